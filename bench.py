@@ -1,0 +1,332 @@
+"""Benchmark of the quantized decode hot path on one MI355X.
+
+Timed workload (the configuration the metric is quoted on):
+one q4 quantized-MLP decode step at Llama-3-8B shapes -- hidden 4096,
+intermediate 14336, group 64, fp16 scales and zero points, batch M=1:
+    residual add + RMSNorm      (mk_residual_rms_norm)
+    gate/up q4 matvec + SwiGLU  (mk_q4_gate_up, 2 x 14336x4096)
+    down q4 matvec + residual   (mk_q4_matvec, 4096x14336)
+Each step uses the next of several distinct weight sets (>= 512 MB in total)
+so the 256 MB Infinity Cache cannot serve the weights; each step is one
+HIP-graph replay, so host launch overhead is not in the timed region.
+
+value = algorithmic HBM bytes of the step (packed codes + fp16 scales/zeros +
+activations in/out) / measured step time, in GB/s.  The JSON line also
+carries:
+  roofline      -- the dominant kernel (q4 gate/up) timed alone with HIP
+                   events, against the 8 TB/s HBM peak;
+  cpu_baseline  -- the numpy oracle (the reference's array path restated)
+                   timed on this host for a bounded sample of the same step;
+  extra         -- M=4/8 and q8 variants, and paged GQA decode attention at
+                   BASELINE config 3 (tok/s and HBM fraction).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mlx-metal-kernels_amd"))
+
+PEAK_GBS = 8000.0
+HIDDEN, INTER, GROUP = 4096, 14336, 64
+
+
+def _parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=30)
+    ap.add_argument("--sets", type=int, default=6, help="distinct weight sets rotated through (>= 512 MB total)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-extra", action="store_true", help="skip the M=4/8, q8 and attention extras")
+    return ap.parse_args()
+
+
+# ----------------------------------------------------------------- inputs
+
+
+def quantize_on_gpu(W, bits, g):
+    """Symmetric groupwise quantization (models/quantize_weights.py:164-203
+    semantics) done with torch ops on the device, for synthetic weights."""
+    import torch
+
+    N, K = W.shape
+    limit = 7 if bits == 4 else 127
+    zp = 8 if bits == 4 else 128
+    Wg = W.float().reshape(N, K // g, g)
+    scale = torch.clamp(Wg.abs().amax(dim=-1) / limit, min=1e-8)
+    q = torch.clamp(torch.round(Wg / scale[..., None]), -limit, limit).to(torch.int32) + zp
+    q = q.reshape(N, K).to(torch.uint8)
+    if bits == 4:
+        q = (q[:, 0::2] | (q[:, 1::2] << 4)).contiguous()
+    s = scale.to(torch.float16).contiguous()
+    z = torch.full_like(s, float(zp))
+    return q, s, z
+
+
+def make_mlp_set(dev, bits, seed):
+    import torch
+
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    mats = []
+    for n, k in ((INTER, HIDDEN), (INTER, HIDDEN), (HIDDEN, INTER)):
+        W = torch.randn((n, k), generator=gen, device=dev, dtype=torch.float32) * 0.02
+        mats.append(quantize_on_gpu(W, bits, GROUP))
+        del W
+    return mats
+
+
+def mlp_bytes(M, bits):
+    """Algorithmic HBM bytes of one MLP step (matches the launches above)."""
+    G_h, G_i = HIDDEN // GROUP, INTER // GROUP
+    code = bits / 8
+    gate_up = 2 * (INTER * HIDDEN * code + INTER * G_h * 4) + M * HIDDEN * 2 + M * INTER * 2
+    down = HIDDEN * INTER * code + HIDDEN * G_i * 4 + M * INTER * 2 + 2 * M * HIDDEN * 2
+    prologue = 5 * M * HIDDEN * 2
+    return int(gate_up), int(down), int(prologue)
+
+
+# ----------------------------------------------------------------- timing helpers
+
+
+def capture(fn):
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm the allocator outside the graph
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graphs(graphs, steps, warmup):
+    """Replay graphs round-robin: warmup untimed, then exactly `steps`
+    replays bracketed by synchronize; returns ms per replay."""
+    import torch
+
+    for i in range(warmup):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+# ----------------------------------------------------------------- workloads
+
+
+def mlp_step_fns(sets, M, bits, dev):
+    import torch
+
+    import mk.norm_ops as norm
+    import mk.quant_ops as qo
+
+    x = torch.randn((M, 1, HIDDEN), device=dev).to(torch.float16)
+    res = torch.randn((M, 1, HIDDEN), device=dev).to(torch.float16)
+    nw = torch.ones(HIDDEN, device=dev, dtype=torch.float16)
+    outs = {}
+
+    def make(ws):
+        (gw, gs, gz), (uw, us, uz), (dw, ds, dz) = ws
+
+        def step():
+            z, n = norm.residual_rms_norm(x, res, nw)
+            mlp = qo.q_gate_up_swiglu(n, gw, uw, gs, us, gz, uz, bits=bits, group_size=GROUP)
+            _, out = qo.q_matvec_residual(mlp, dw, ds, dz, z, bits=bits, group_size=GROUP)
+            outs["out"] = out
+
+        def gate_up_only():
+            qo.q_gate_up_swiglu(x, gw, uw, gs, us, gz, uz, bits=bits, group_size=GROUP)
+
+        return step, gate_up_only
+
+    return [make(ws) for ws in sets], (x, res, nw)
+
+
+def attention_config3(dev, steps, warmup):
+    """B=16, Hq 32 / Hkv 8, D=128, P=16, lengths U[512,8192]
+    (seed 3), block table a seeded permutation (seed 4); fp16 K/V ~ N(0,1).
+    Rotates two cache copies (>= 256 MB each) to defeat the Infinity Cache."""
+    import numpy as np
+    import torch
+
+    import mk.gqa_ops as gqa
+
+    B, Hq, Hkv, D, P, mb = 16, 32, 8, 128, 16, 512
+    rng = np.random.default_rng(3)
+    lengths = rng.integers(512, 8193, size=B).astype(np.int32)
+    NP = B * mb
+    bt = torch.from_numpy(np.random.default_rng(4).permutation(NP).astype(np.int32).reshape(B, mb)).to(dev)
+    ln = torch.from_numpy(lengths).to(dev)
+    q = torch.randn((B, 1, Hq, D), device=dev).to(torch.float16)
+    caches = []
+    for c in range(3):
+        Kp = torch.randn((NP, P, Hkv, D), device=dev).to(torch.float16)
+        Vp = torch.randn((NP, P, Hkv, D), device=dev).to(torch.float16)
+        caches.append((Kp, Vp))
+    graphs = [capture(lambda K=K, V=V: gqa.paged_gqa_decode_attention(q, K, V, bt, ln)) for K, V in caches]
+    ms = time_graphs(graphs, steps, warmup)
+    tot = int(lengths.sum())
+    nbytes = tot * Hkv * D * 2 * 2 + sum(math.ceil(int(n) / P) for n in lengths) * 4 + B * Hq * D * 2 * 2 + B * 4
+    del caches, graphs
+    torch.cuda.empty_cache()
+    return {
+        "workload": "config3_paged_gqa_fp16_B16_ctx_U512_8192",
+        "tokens_per_s": B / (ms * 1e-3),
+        "us_per_call": ms * 1e3,
+        "kv_tokens": tot,
+        "ns_per_kv_token": ms * 1e6 / tot,
+        "hbm_gbs": nbytes / (ms * 1e-3) / 1e9,
+        "frac_of_peak": nbytes / (ms * 1e-3) / 1e9 / PEAK_GBS,
+        "bytes": nbytes,
+    }
+
+
+# ----------------------------------------------------------------- CPU baseline
+
+
+def cpu_baseline(sets, x_res_nw, budget_s=20.0):
+    """The numpy oracle's MLP step (dequantize to fp16, fp32 matmul -- the
+    reference's pure-array path) on this host, one weight set, bounded."""
+    import numpy as np
+
+    from oracle import quant as oq
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        blas = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # noqa: BLE001
+        blas = 1
+    (gw, gs, gz), (uw, us, uz), (dw, ds, dz) = sets[0]
+    cpu = lambda t: t.cpu().numpy()
+    g = (cpu(gw), cpu(gs).astype(np.float32), cpu(gz).astype(np.float32))
+    u = (cpu(uw), cpu(us).astype(np.float32), cpu(uz).astype(np.float32))
+    d = (cpu(dw), cpu(ds).astype(np.float32), cpu(dz).astype(np.float32))
+    x, res, nw = (cpu(t) for t in x_res_nw)
+    x2, r2 = x.reshape(-1, HIDDEN), res.reshape(-1, HIDDEN)
+    oq.mlp_block(x2, r2, nw, g, u, d, bits=4, group_size=GROUP)  # warm
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 2:
+        t0 = time.perf_counter()
+        oq.mlp_block(x2, r2, nw, g, u, d, bits=4, group_size=GROUP)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 20:
+            break
+    med = sorted(times)[len(times) // 2]
+    return med, len(times), blas
+
+
+# ----------------------------------------------------------------- main
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build targets one GPU; multi-GPU runs are not part of it",
+                          "requested_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+
+    from mk import _lib
+
+    dev = torch.device("cuda:0")
+    _lib.load()
+    torch.manual_seed(0)
+
+    sets = [make_mlp_set(dev, 4, 100 + i) for i in range(args.sets)]
+    set_bytes = sum(t.numel() * t.element_size() for ws in sets for m in ws for t in m)
+    fns, x_res_nw = mlp_step_fns(sets, 1, 4, dev)
+    step_graphs = [capture(step) for step, _ in fns]
+    gu_graphs = [capture(gu) for _, gu in fns]
+
+    # timed region: exactly `steps` MLP steps
+    ms = time_graphs(step_graphs, args.steps, args.warmup)
+    b_gu, b_down, b_pro = mlp_bytes(1, 4)
+    step_bytes = b_gu + b_down + b_pro
+    value = step_bytes / (ms * 1e-3) / 1e9
+
+    # dominant kernel alone (same stream, HIP events over the timed region)
+    ms_gu = time_graphs(gu_graphs, args.steps, args.warmup)
+    gu_alone_bytes = b_gu - 1 * INTER * 2 + 0  # x read from the input, mlp written; no prologue
+    achieved = b_gu / (ms_gu * 1e-3) / 1e9
+
+    extra = {}
+    if not args.no_extra:
+        for bits, M in ((4, 4), (4, 8), (8, 1)):
+            if bits == 8:
+                s8 = [make_mlp_set(dev, 8, 200 + i) for i in range(4)]
+                f8, _ = mlp_step_fns(s8, M, 8, dev)
+            else:
+                f8, _ = mlp_step_fns(sets, M, 4, dev)
+            gr = [capture(step) for step, _ in f8]
+            m_ms = time_graphs(gr, max(50, args.steps // 3), 10)
+            bb = sum(mlp_bytes(M, bits))
+            extra[f"q{bits}_mlp_M{M}"] = {"us_per_step": m_ms * 1e3, "hbm_gbs": bb / (m_ms * 1e-3) / 1e9,
+                                          "frac_of_peak": bb / (m_ms * 1e-3) / 1e9 / PEAK_GBS}
+            del gr, f8
+            if bits == 8:
+                del s8
+            torch.cuda.empty_cache()
+        del step_graphs, gu_graphs
+        torch.cuda.empty_cache()
+        extra["paged_attention"] = attention_config3(dev, max(50, args.steps // 3), 10)
+
+    cpu = None
+    if not args.no_cpu:
+        med, reps, blas = cpu_baseline(sets, x_res_nw)
+        cpu = {
+            "value": step_bytes / med / 1e9,
+            "unit": "GB/s",
+            "cores": blas,
+            "kind": "port",
+            "sample": f"{reps} q4 MLP decode steps (M=1, 4096/14336, g64) of the numpy oracle, median "
+                      f"{med * 1e3:.1f} ms/step; BLAS threads {blas}, host cpu_count {os.cpu_count()}",
+        }
+
+    line = {
+        "metric": "q4 GEMV HBM GB/s (% of peak) + paged GQA decode tok/s at Llama-3-8B shapes",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (random N(0,0.02) weights quantized q4 g64 on device; random activations)",
+        "config": {"workload": "config2_q4_mlp_decode_step_M1", "hidden": HIDDEN, "intermediate": INTER,
+                   "group_size": GROUP, "M": 1, "weight_sets": args.sets, "weight_set_bytes_total": set_bytes,
+                   "step_bytes": step_bytes, "frac_of_peak": round(value / PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_mfma_kernel q4 gate/up+SwiGLU 2x14336x4096 M=1",
+                     "bytes_per_launch": b_gu, "us_per_launch": round(ms_gu * 1e3, 3)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

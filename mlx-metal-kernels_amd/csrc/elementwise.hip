@@ -1,0 +1,160 @@
+// Elementwise prologue/epilogue kernels of the quantized MLP block.
+//
+// swiglu / fused_swiglu  ops/activation_ops.py:83-153   out = g/(1+exp(-g))*u
+// residual_add           ops/fused_ops.py:149-180        out = x + r
+// rms_norm               ops/norm_ops.py:47-85           y = x*rsqrt(mean(x^2)+eps)*w
+// residual + rms_norm    ops/mlp_block_ops.py:343-344    (z = x + r; y = rms_norm(z))
+// All math is fp32 with one rounding into the storage type per output, as the
+// reference's astype() chain does.  These are O(hidden) per token -- noise next
+// to the matvecs -- so they stay simple grid-stride loops.
+#include "common.h"
+
+namespace {
+
+template <typename T>
+__device__ __forceinline__ float silu_mul(T g, T u) {
+  const float gf = to_f32(g);
+  return gf / (1.0f + expf(-gf)) * to_f32(u);
+}
+
+template <typename T>
+__global__ void swiglu_kernel(const T* __restrict__ g, const T* __restrict__ u, T* __restrict__ out,
+                              int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = from_f32<T>(silu_mul(g[i], u[i]));
+}
+
+template <typename T>
+__global__ void residual_add_kernel(const T* __restrict__ x, const T* __restrict__ r,
+                                    T* __restrict__ out, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = from_f32<T>(to_f32(x[i]) + to_f32(r[i]));
+}
+
+// One workgroup (256 threads) per row.  With RES, z = x + r is rounded to T,
+// stored, and the norm is taken over the rounded z (the reference normalizes
+// the materialized z).
+template <typename T, typename WT, bool RES>
+__global__ __launch_bounds__(256) void rms_norm_kernel(const T* __restrict__ x,
+                                                       const T* __restrict__ r,
+                                                       const WT* __restrict__ w,
+                                                       T* __restrict__ z_out, T* __restrict__ y,
+                                                       int64_t D, float eps) {
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * D;
+  const T* rr = RES ? r + row * D : nullptr;
+  T* zr = RES ? z_out + row * D : nullptr;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < D; i += blockDim.x) {
+    float v = to_f32(xr[i]);
+    if constexpr (RES) {
+      const T zt = from_f32<T>(v + to_f32(rr[i]));
+      zr[i] = zt;
+      v = to_f32(zt);
+    }
+    ss += v * v;
+  }
+  __shared__ float part[4];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = part[0] + part[1] + part[2] + part[3];
+  const float inv = rsqrtf(tot / (float)D + eps);
+  T* yr = y + row * D;
+  const T* src = RES ? zr : xr;
+  for (int64_t i = threadIdx.x; i < D; i += blockDim.x) {
+    // each thread re-reads the z it wrote itself, so no barrier is needed
+    const float v = to_f32(src[i]);
+    yr[i] = from_f32<T>(v * inv * to_f32(w[i]));
+  }
+}
+
+inline dim3 grid_for(int64_t work, int threads) {
+  int64_t b = (work + threads - 1) / threads;
+  if (b > 65536) b = 65536;
+  if (b < 1) b = 1;
+  return dim3((unsigned)b);
+}
+
+template <bool RES>
+int norm_entry(const void* x, const void* r, const void* w, void* z, void* y, int64_t rows,
+               int64_t D, float eps, int xdt, int wdt, void* stream) {
+  MK_REQUIRE(x && w && y && rows >= 0 && D > 0);
+  MK_REQUIRE(!RES || (r && z));
+  MK_REQUIRE(xdt == MK_DT_F16 || xdt == MK_DT_BF16 || (xdt == MK_DT_F32 && !RES));
+  MK_REQUIRE(wdt == MK_DT_F16 || wdt == MK_DT_BF16 || wdt == MK_DT_F32);
+  MK_REQUIRE(rows < (1LL << 31));
+  if (rows == 0) return MK_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)rows);
+#define MK_NORM(T, WT)                                                                       \
+  rms_norm_kernel<T, WT, RES><<<grid, 256, 0, st>>>((const T*)x, (const T*)r, (const WT*)w, \
+                                                    (T*)z, (T*)y, D, eps)
+  if (xdt == MK_DT_F16) {
+    if (wdt == MK_DT_F16) MK_NORM(f16, f16);
+    else if (wdt == MK_DT_BF16) MK_NORM(f16, bf16);
+    else MK_NORM(f16, float);
+  } else if (xdt == MK_DT_BF16) {
+    if (wdt == MK_DT_F16) MK_NORM(bf16, f16);
+    else if (wdt == MK_DT_BF16) MK_NORM(bf16, bf16);
+    else MK_NORM(bf16, float);
+  } else {
+    if (wdt == MK_DT_F16) MK_NORM(float, f16);
+    else if (wdt == MK_DT_BF16) MK_NORM(float, bf16);
+    else MK_NORM(float, float);
+  }
+#undef MK_NORM
+  MK_CHECK_LAUNCH();
+  return MK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mk_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream) {
+  MK_REQUIRE(gate && up && out && n >= 0);
+  MK_REQUIRE(dtype == MK_DT_F16 || dtype == MK_DT_BF16);
+  if (n == 0) return MK_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == MK_DT_F16)
+    swiglu_kernel<f16><<<grid_for(n, 256), 256, 0, st>>>((const f16*)gate, (const f16*)up,
+                                                         (f16*)out, n);
+  else
+    swiglu_kernel<bf16><<<grid_for(n, 256), 256, 0, st>>>((const bf16*)gate, (const bf16*)up,
+                                                          (bf16*)out, n);
+  MK_CHECK_LAUNCH();
+  return MK_OK;
+}
+
+int mk_residual_add(const void* x, const void* residual, void* out, int64_t n, int dtype,
+                    void* stream) {
+  MK_REQUIRE(x && residual && out && n >= 0);
+  MK_REQUIRE(dtype == MK_DT_F16 || dtype == MK_DT_BF16);
+  if (n == 0) return MK_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == MK_DT_F16)
+    residual_add_kernel<f16><<<grid_for(n, 256), 256, 0, st>>>((const f16*)x, (const f16*)residual,
+                                                               (f16*)out, n);
+  else
+    residual_add_kernel<bf16><<<grid_for(n, 256), 256, 0, st>>>(
+        (const bf16*)x, (const bf16*)residual, (bf16*)out, n);
+  MK_CHECK_LAUNCH();
+  return MK_OK;
+}
+
+int mk_rms_norm(const void* x, const void* weight, void* y, int64_t rows, int64_t D, float eps,
+                int x_dtype, int w_dtype, void* stream) {
+  return norm_entry<false>(x, nullptr, weight, nullptr, y, rows, D, eps, x_dtype, w_dtype, stream);
+}
+
+int mk_residual_rms_norm(const void* x, const void* residual, const void* weight, void* z_out,
+                         void* y_out, int64_t rows, int64_t D, float eps, int x_dtype,
+                         int w_dtype, void* stream) {
+  return norm_entry<true>(x, residual, weight, z_out, y_out, rows, D, eps, x_dtype, w_dtype,
+                          stream);
+}
+
+}  // extern "C"

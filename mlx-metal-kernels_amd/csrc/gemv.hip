@@ -1,0 +1,602 @@
+// Groupwise-affine q4/q8 decode matvec family for gfx950.
+//
+// Semantics (ops/quant_ops.py:509-526, 574-588, 634-738):
+//   y[m,n] = clip(sum_k x[m,k] * W[n,k], +-max(act)) rounded to the activation
+//   type, W[n,k] = (q[n,k] - z[n,k/g]) * s[n,k/g].
+// q4 codes are packed two per byte (low nibble = even k), so on little-endian
+// hardware a 32-bit word holds 8 consecutive codes, nibble i at bits 4i.
+//
+// Fast path (M <= 16 per launch, K % 64 == 0 for q4 / % 32 for q8, power-of-two
+// group size >= 16 (q4) / >= 8 (q8)):
+//   * one workgroup owns a 16-row output tile; its KW waves split K;
+//   * lane (n = l%16, kb = l/16) streams 32 contiguous code bytes of row n per
+//     chunk with two 128-bit loads, dequantizes them in registers and feeds
+//     v_mfma_f32_16x16x32_{f16,bf16} with A = W tile (16 n x 32 k) and
+//     B = x^T tile (32 k x 16 m); decode batches M < 16 pad B with zeros;
+//   * the waves' partial 16x16 tiles are summed through LDS; the epilogue
+//     saturates, and optionally fuses SwiGLU (gate/up) or a residual add.
+// fp16 activations with fp16 scales use an exponent-magic dequant: a code c
+// OR'ed into the mantissa of 1024.0h gives 1024+c exactly, so
+//   w = fma(c, s, -z*s)  (two packed-f16 ops per pair of weights).
+// The MFMA contraction is order-free in k, so the activation operand is built
+// in the same permuted k order the magic unpack produces.
+#include "common.h"
+
+namespace {
+
+constexpr int EPI_NONE = 0;
+constexpr int EPI_RESIDUAL = 1;
+constexpr int EPI_GATE_UP = 2;
+
+template <int BITS>
+struct QFmt {
+  static constexpr int KL = BITS == 4 ? 64 : 32;     // k per lane chunk (32 code bytes)
+  static constexpr int KC = 4 * KL;                  // k per wave chunk
+  static constexpr int STEPS = BITS == 4 ? 8 : 4;    // MFMA k32 steps per chunk
+  static constexpr int ROW_BYTES_NUM = BITS;         // row bytes = K * BITS / 8
+};
+
+// --------------------------------------------------------------------------
+// activation operand: 8 halves of x for one MFMA step, in the k order the
+// weight unpack produces.
+// --------------------------------------------------------------------------
+template <int BITS, bool MAGIC>
+__device__ __forceinline__ u32x4 xperm(u32x4 X) {
+  if constexpr (!MAGIC) {
+    return X;  // natural order
+  } else if constexpr (BITS == 4) {
+    // weight order [0,4,1,5,2,6,3,7]
+    u32x4 r;
+    r[0] = (X[0] & 0xFFFFu) | (X[2] << 16);
+    r[1] = (X[0] >> 16) | (X[2] & 0xFFFF0000u);
+    r[2] = (X[1] & 0xFFFFu) | (X[3] << 16);
+    r[3] = (X[1] >> 16) | (X[3] & 0xFFFF0000u);
+    return r;
+  } else {
+    // weight order [0,2,1,3,4,6,5,7]
+    u32x4 r;
+    r[0] = (X[0] & 0xFFFFu) | (X[1] << 16);
+    r[1] = (X[0] >> 16) | (X[1] & 0xFFFF0000u);
+    r[2] = (X[2] & 0xFFFFu) | (X[3] << 16);
+    r[3] = (X[2] >> 16) | (X[3] & 0xFFFF0000u);
+    return r;
+  }
+}
+
+// Per-group dequant parameters.
+struct GpMagic {
+  f16x2 s;    // (s, s)
+  f16x2 s16;  // (s/16, s/16)  for codes sitting at nibble bits 4..7
+  f16x2 nzs;  // (-z*s, -z*s)
+};
+struct GpExact {
+  float s;
+  float z;
+};
+
+__device__ __forceinline__ f16x2 h2(f16 v) { return (f16x2){v, v}; }
+
+__device__ __forceinline__ GpMagic make_gp_magic(f16 s, f16 z) {
+  GpMagic g;
+  g.s = h2(s);
+  g.s16 = h2(s * (f16)0.0625f);
+  g.nzs = h2(-(z * s));
+  return g;
+}
+
+// q4 word (8 codes) -> 8 fp16 weights in order [0,4,1,5,2,6,3,7].
+__device__ __forceinline__ u32x4 dq4_magic(uint32_t u, const GpMagic& g) {
+  const f16x2 k1024 = {(f16)1024.0f, (f16)1024.0f};
+  const uint32_t v = u >> 8;
+  f16x2 a = bitcast<f16x2>((u & 0x000F000Fu) | 0x64006400u) - k1024;  // c0, c4
+  f16x2 b = bitcast<f16x2>((u & 0x00F000F0u) | 0x64006400u) - k1024;  // 16*c1, 16*c5
+  f16x2 c = bitcast<f16x2>((v & 0x000F000Fu) | 0x64006400u) - k1024;  // c2, c6
+  f16x2 d = bitcast<f16x2>((v & 0x00F000F0u) | 0x64006400u) - k1024;  // 16*c3, 16*c7
+  a = __builtin_elementwise_fma(a, g.s, g.nzs);
+  b = __builtin_elementwise_fma(b, g.s16, g.nzs);
+  c = __builtin_elementwise_fma(c, g.s, g.nzs);
+  d = __builtin_elementwise_fma(d, g.s16, g.nzs);
+  u32x4 r;
+  r[0] = bitcast<uint32_t>(a);
+  r[1] = bitcast<uint32_t>(b);
+  r[2] = bitcast<uint32_t>(c);
+  r[3] = bitcast<uint32_t>(d);
+  return r;
+}
+
+// two q8 words (8 codes) -> 8 fp16 weights in order [0,2,1,3,4,6,5,7].
+__device__ __forceinline__ u32x4 dq8_magic(uint32_t u0, uint32_t u1, const GpMagic& g) {
+  const f16x2 k1024 = {(f16)1024.0f, (f16)1024.0f};
+  f16x2 a0 = bitcast<f16x2>((u0 & 0x00FF00FFu) | 0x64006400u) - k1024;
+  f16x2 b0 = bitcast<f16x2>(((u0 >> 8) & 0x00FF00FFu) | 0x64006400u) - k1024;
+  f16x2 a1 = bitcast<f16x2>((u1 & 0x00FF00FFu) | 0x64006400u) - k1024;
+  f16x2 b1 = bitcast<f16x2>(((u1 >> 8) & 0x00FF00FFu) | 0x64006400u) - k1024;
+  a0 = __builtin_elementwise_fma(a0, g.s, g.nzs);
+  b0 = __builtin_elementwise_fma(b0, g.s, g.nzs);
+  a1 = __builtin_elementwise_fma(a1, g.s, g.nzs);
+  b1 = __builtin_elementwise_fma(b1, g.s, g.nzs);
+  u32x4 r;
+  r[0] = bitcast<uint32_t>(a0);
+  r[1] = bitcast<uint32_t>(b0);
+  r[2] = bitcast<uint32_t>(a1);
+  r[3] = bitcast<uint32_t>(b1);
+  return r;
+}
+
+// Exact path: w = AT((q - z) * s) computed in fp32, natural k order.
+template <typename AT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  AT a = from_f32<AT>(lo), b = from_f32<AT>(hi);
+  return (uint32_t)bitcast<uint16_t>(a) | ((uint32_t)bitcast<uint16_t>(b) << 16);
+}
+
+template <typename AT>
+__device__ __forceinline__ u32x4 dq4_exact(uint32_t u, const GpExact& g) {
+  float w[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) w[e] = ((float)((u >> (4 * e)) & 15u) - g.z) * g.s;
+  u32x4 r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) r[p] = pack2<AT>(w[2 * p], w[2 * p + 1]);
+  return r;
+}
+
+template <typename AT>
+__device__ __forceinline__ u32x4 dq8_exact(uint32_t u0, uint32_t u1, const GpExact& g) {
+  float w[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) w[e] = ((float)((u0 >> (8 * e)) & 255u) - g.z) * g.s;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) w[4 + e] = ((float)((u1 >> (8 * e)) & 255u) - g.z) * g.s;
+  u32x4 r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) r[p] = pack2<AT>(w[2 * p], w[2 * p + 1]);
+  return r;
+}
+
+template <typename AT>
+__device__ __forceinline__ f32x4 mfma_k32(u32x4 a, u32x4 b, f32x4 c);
+
+template <>
+__device__ __forceinline__ f32x4 mfma_k32<f16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<f16x8>(a), bitcast<f16x8>(b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma_k32<bf16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(bitcast<bf16x8>(a), bitcast<bf16x8>(b), c, 0, 0,
+                                                 0);
+}
+
+template <typename ST>
+__device__ __forceinline__ float ld_scalar_f32(const ST* p) {
+  return to_f32(*p);
+}
+
+struct GemvArgs {
+  const void* x;         // [M, K]
+  const uint8_t* w[2];   // [N, row_bytes]
+  const void* s[2];      // [N, G]
+  const void* z[2];      // [N, G] or null
+  const void* residual;  // [M, N] or null
+  void* y0;              // EPI_NONE: y; EPI_RESIDUAL: y_mm (nullable); GATE_UP: gate (nullable)
+  void* y1;              // EPI_RESIDUAL: out;  GATE_UP: up (nullable)
+  void* y2;              // GATE_UP: mlp (nullable)
+  int M, N, K;
+  int row_bytes;
+  int G;
+  int lg;                // log2(group size)
+  int kw;                // waves per workgroup (K split)
+};
+
+// --------------------------------------------------------------------------
+// fast MFMA kernel
+// --------------------------------------------------------------------------
+template <int BITS, typename AT, typename ST, bool MAGIC, int GPC, int NMAT, int EPI>
+__global__ __launch_bounds__(512) void gemv_mfma_kernel(const GemvArgs args) {
+  using F = QFmt<BITS>;
+  constexpr int STEPS = F::STEPS;
+  constexpr int SPG = STEPS / GPC;  // MFMA steps per quantization group
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int kw = args.kw;
+  const int M = args.M, N = args.N, K = args.K;
+
+  const int n0 = blockIdx.x * 16;
+  const int nl = lane & 15;
+  const int kb = lane >> 4;
+  const int n = n0 + nl;
+  const int n_ld = n < N ? n : N - 1;  // rows past N load a valid row; results discarded
+  const int m = lane & 15;
+  const bool x_active = m < M;
+
+  // this wave's chunk range
+  const int chunks = (K + F::KC - 1) / F::KC;
+  const int c_begin = (chunks * wave) / kw;
+  const int c_end = (chunks * (wave + 1)) / kw;
+
+  const uint8_t* wrow[NMAT];
+  const ST* srow[NMAT];
+  const ST* zrow[NMAT];
+#pragma unroll
+  for (int t = 0; t < NMAT; ++t) {
+    wrow[t] = args.w[t] + (size_t)n_ld * args.row_bytes + kb * 32;
+    srow[t] = reinterpret_cast<const ST*>(args.s[t]) + (size_t)n_ld * args.G;
+    zrow[t] = args.z[t] ? reinterpret_cast<const ST*>(args.z[t]) + (size_t)n_ld * args.G : nullptr;
+  }
+  const AT* xrow = reinterpret_cast<const AT*>(args.x) + (size_t)(x_active ? m : 0) * K + kb * F::KL;
+
+  f32x4 acc[NMAT];
+#pragma unroll
+  for (int t = 0; t < NMAT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  for (int c = c_begin; c < c_end; ++c) {
+    const int k0 = c * F::KC + kb * F::KL;  // first k of this lane's chunk
+    const bool valid = k0 < K;
+
+    // ---- loads (issued together so they are in flight at once)
+    u32x4 wv[NMAT][2];
+    u32x4 xv[STEPS];
+    ST sv[NMAT][GPC], zv[NMAT][GPC];
+    if (valid) {
+      const size_t boff = (size_t)c * (F::KC * BITS / 8);
+#pragma unroll
+      for (int t = 0; t < NMAT; ++t) {
+        wv[t][0] = ldg128_stream(wrow[t] + boff);
+        wv[t][1] = ldg128_stream(wrow[t] + boff + 16);
+      }
+      const int g0 = k0 >> args.lg;
+#pragma unroll
+      for (int t = 0; t < NMAT; ++t) {
+#pragma unroll
+        for (int j = 0; j < GPC; ++j) {
+          sv[t][j] = srow[t][g0 + j];
+          zv[t][j] = zrow[t] ? zrow[t][g0 + j] : (ST)0.0f;
+        }
+      }
+      if (x_active) {
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) xv[s] = ldg128(xrow + (size_t)c * F::KC + 8 * s);
+      } else {
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) xv[s] = (u32x4){0u, 0u, 0u, 0u};
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < NMAT; ++t) {
+        wv[t][0] = (u32x4){0u, 0u, 0u, 0u};
+        wv[t][1] = (u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int j = 0; j < GPC; ++j) {
+          sv[t][j] = (ST)0.0f;
+          zv[t][j] = (ST)0.0f;
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s) xv[s] = (u32x4){0u, 0u, 0u, 0u};
+    }
+
+    // ---- dequant + MFMA
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const u32x4 b = xperm<BITS, MAGIC>(xv[s]);
+      const int j = s / SPG;
+#pragma unroll
+      for (int t = 0; t < NMAT; ++t) {
+        u32x4 a;
+        if constexpr (MAGIC) {
+          const GpMagic gp = make_gp_magic((f16)sv[t][j], (f16)zv[t][j]);
+          if constexpr (BITS == 4) {
+            a = dq4_magic(wv[t][s >> 2][s & 3], gp);
+          } else {
+            a = dq8_magic(wv[t][s >> 1][(2 * s) & 3], wv[t][s >> 1][(2 * s + 1) & 3], gp);
+          }
+        } else {
+          GpExact gp;
+          gp.s = to_f32(sv[t][j]);
+          gp.z = to_f32(zv[t][j]);
+          if constexpr (BITS == 4) {
+            a = dq4_exact<AT>(wv[t][s >> 2][s & 3], gp);
+          } else {
+            a = dq8_exact<AT>(wv[t][s >> 1][(2 * s) & 3], wv[t][s >> 1][(2 * s + 1) & 3], gp);
+          }
+        }
+        acc[t] = mfma_k32<AT>(a, b, acc[t]);
+      }
+    }
+  }
+
+  // ---- cross-wave reduction through LDS
+  __shared__ f32x4 red[NMAT][8][64];
+#pragma unroll
+  for (int t = 0; t < NMAT; ++t) red[t][wave][lane] = acc[t];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int t = 0; t < NMAT; ++t) {
+    f32x4 v = red[t][0][lane];
+    for (int w = 1; w < kw; ++w) v += red[t][w][lane];
+    acc[t] = v;
+  }
+
+  // ---- epilogue: lane holds D[n = nb + i][m], i = 0..3
+  if (!x_active) return;
+  const int nb = n0 + 4 * kb;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int nn = nb + i;
+    if (nn >= N) break;
+    const size_t o = (size_t)m * N + nn;
+    if constexpr (EPI == EPI_NONE) {
+      reinterpret_cast<AT*>(args.y0)[o] = saturate_cast<AT>(acc[0][i]);
+    } else if constexpr (EPI == EPI_RESIDUAL) {
+      const AT d = saturate_cast<AT>(acc[0][i]);
+      if (args.y0) reinterpret_cast<AT*>(args.y0)[o] = d;
+      const float r = to_f32(reinterpret_cast<const AT*>(args.residual)[o]);
+      reinterpret_cast<AT*>(args.y1)[o] = from_f32<AT>(r + to_f32(d));
+    } else {
+      const AT g = saturate_cast<AT>(acc[0][i]);
+      const AT u = saturate_cast<AT>(acc[1][i]);
+      if (args.y0) reinterpret_cast<AT*>(args.y0)[o] = g;
+      if (args.y1) reinterpret_cast<AT*>(args.y1)[o] = u;
+      if (args.y2) {
+        const float gf = to_f32(g);
+        const float sil = gf / (1.0f + expf(-gf));
+        reinterpret_cast<AT*>(args.y2)[o] = from_f32<AT>(sil * to_f32(u));
+      }
+    }
+  }
+}
+
+// --------------------------------------------------------------------------
+// generic kernel: any K (odd K uses ceil(K/2) packed columns), any group size,
+// any M.  One wave per output row; fp32 math with the dequantized weight
+// rounded to the activation type first, as the reference path does
+// (ops/quant_ops.py:523-526).
+// --------------------------------------------------------------------------
+template <int BITS, typename AT, typename ST, int NMAT, int EPI>
+__global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvArgs args, int gs) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= args.N) return;
+  const int K = args.K, M = args.M, N = args.N;
+  const AT* x = reinterpret_cast<const AT*>(args.x);
+  for (int m = 0; m < M; ++m) {
+    float dot[NMAT];
+#pragma unroll
+    for (int t = 0; t < NMAT; ++t) {
+      const uint8_t* wr = args.w[t] + (size_t)n * args.row_bytes;
+      const ST* sr = reinterpret_cast<const ST*>(args.s[t]) + (size_t)n * args.G;
+      const ST* zr = args.z[t] ? reinterpret_cast<const ST*>(args.z[t]) + (size_t)n * args.G : nullptr;
+      float a = 0.f;
+      for (int k = lane; k < K; k += 64) {
+        uint32_t q;
+        if constexpr (BITS == 4) {
+          const uint8_t b = wr[k >> 1];
+          q = (k & 1) ? (b >> 4) : (b & 15u);
+        } else {
+          q = wr[k];
+        }
+        const int g = k / gs;
+        const float s = to_f32(sr[g]);
+        const float z = zr ? to_f32(zr[g]) : 0.0f;
+        const float w = to_f32(from_f32<AT>(((float)q - z) * s));
+        a += to_f32(x[(size_t)m * K + k]) * w;
+      }
+      dot[t] = wave_sum(a);
+    }
+    if (lane != 0) continue;
+    const size_t o = (size_t)m * N + n;
+    if constexpr (EPI == EPI_NONE) {
+      reinterpret_cast<AT*>(args.y0)[o] = saturate_cast<AT>(dot[0]);
+    } else if constexpr (EPI == EPI_RESIDUAL) {
+      const AT d = saturate_cast<AT>(dot[0]);
+      if (args.y0) reinterpret_cast<AT*>(args.y0)[o] = d;
+      const float r = to_f32(reinterpret_cast<const AT*>(args.residual)[o]);
+      reinterpret_cast<AT*>(args.y1)[o] = from_f32<AT>(r + to_f32(d));
+    } else {
+      const AT g = saturate_cast<AT>(dot[0]);
+      const AT u = saturate_cast<AT>(dot[NMAT - 1]);
+      if (args.y0) reinterpret_cast<AT*>(args.y0)[o] = g;
+      if (args.y1) reinterpret_cast<AT*>(args.y1)[o] = u;
+      if (args.y2) {
+        const float gf = to_f32(g);
+        const float sil = gf / (1.0f + expf(-gf));
+        reinterpret_cast<AT*>(args.y2)[o] = from_f32<AT>(sil * to_f32(u));
+      }
+    }
+  }
+}
+
+// --------------------------------------------------------------------------
+// host dispatch
+// --------------------------------------------------------------------------
+inline int ilog2_exact(int64_t v) {
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int l = 0;
+  while ((1LL << l) < v) ++l;
+  return l;
+}
+
+template <int BITS, typename AT, typename ST, bool MAGIC, int NMAT, int EPI>
+int launch_fast(const GemvArgs& a, int gpc, hipStream_t st) {
+  const dim3 grid((a.N + 15) / 16);
+  const dim3 block(64 * a.kw);
+  switch (gpc) {
+    case 1: gemv_mfma_kernel<BITS, AT, ST, MAGIC, 1, NMAT, EPI><<<grid, block, 0, st>>>(a); break;
+    case 2: gemv_mfma_kernel<BITS, AT, ST, MAGIC, 2, NMAT, EPI><<<grid, block, 0, st>>>(a); break;
+    case 4: gemv_mfma_kernel<BITS, AT, ST, MAGIC, 4, NMAT, EPI><<<grid, block, 0, st>>>(a); break;
+    default: return MK_ERR_UNSUPPORTED;
+  }
+  MK_CHECK_LAUNCH();
+  return MK_OK;
+}
+
+template <int BITS, typename AT, typename ST, int NMAT, int EPI>
+int launch_generic(const GemvArgs& a, int gs, hipStream_t st) {
+  const dim3 grid((a.N + 3) / 4);
+  gemv_generic_kernel<BITS, AT, ST, NMAT, EPI><<<grid, dim3(256), 0, st>>>(a, gs);
+  MK_CHECK_LAUNCH();
+  return MK_OK;
+}
+
+// Waves per workgroup: enough K-parallelism to keep >= ~4 waves per SIMD
+// in flight on 256 CUs, without giving a wave less than one chunk.
+inline int choose_kw(int64_t N, int64_t K, int kc) {
+  const int64_t tiles = (N + 15) / 16;
+  const int64_t chunks = (K + kc - 1) / kc;
+  int kw = tiles >= 1024 ? 4 : 8;
+  if (kw > chunks) kw = (int)chunks;
+  if (kw < 1) kw = 1;
+  return kw;
+}
+
+template <int BITS, int NMAT, int EPI>
+int gemv_dispatch(GemvArgs a, int64_t M, int64_t N, int64_t K, int64_t gs, int act_dt, int sc_dt,
+                  hipStream_t st) {
+  using F = QFmt<BITS>;
+  MK_REQUIRE(M >= 0 && N > 0 && K > 0 && gs > 0);
+  MK_REQUIRE(act_dt == MK_DT_F16 || act_dt == MK_DT_BF16);
+  MK_REQUIRE(sc_dt == MK_DT_F16 || sc_dt == MK_DT_F32);
+  MK_REQUIRE(N < (1LL << 31) && K < (1LL << 31));
+  if (M == 0) return MK_OK;
+  for (int t = 0; t < NMAT; ++t) MK_REQUIRE(a.w[t] && a.s[t]);
+  MK_REQUIRE(a.x);
+
+  a.N = (int)N;
+  a.K = (int)K;
+  a.G = (int)((K + gs - 1) / gs);
+  a.row_bytes = BITS == 4 ? (int)((K + 1) / 2) : (int)K;
+
+  const int lg = ilog2_exact(gs);
+  int gpc = 0;
+  if (lg >= 0) {
+    if (gs >= F::KL) gpc = 1;
+    else if (gs >= 8 && F::KL / gs <= 4) gpc = (int)(F::KL / gs);
+  }
+  bool fast = gpc > 0 && (K % F::KL) == 0 && mk_aligned(a.x, 16);
+  for (int t = 0; t < NMAT; ++t) fast = fast && mk_aligned(a.w[t], 16);
+  a.lg = lg;
+
+  const int64_t mblocks = (M + 15) / 16;
+  const size_t xe = 2;  // activation element size
+  int rc = MK_OK;
+  for (int64_t mb = 0; mb < mblocks && rc == MK_OK; ++mb) {
+    GemvArgs b = a;
+    const int64_t m0 = mb * 16;
+    const int64_t mrows = (M - m0) < 16 ? (M - m0) : 16;
+    b.M = (int)mrows;
+    b.x = (const char*)a.x + (size_t)m0 * K * xe;
+    if (a.residual) b.residual = (const char*)a.residual + (size_t)m0 * N * xe;
+    if (a.y0) b.y0 = (char*)a.y0 + (size_t)m0 * N * xe;
+    if (a.y1) b.y1 = (char*)a.y1 + (size_t)m0 * N * xe;
+    if (a.y2) b.y2 = (char*)a.y2 + (size_t)m0 * N * xe;
+    if (fast) {
+      b.kw = choose_kw(N, K, F::KC);
+      if (act_dt == MK_DT_F16 && sc_dt == MK_DT_F16)
+        rc = launch_fast<BITS, f16, f16, true, NMAT, EPI>(b, gpc, st);
+      else if (act_dt == MK_DT_F16)
+        rc = launch_fast<BITS, f16, float, false, NMAT, EPI>(b, gpc, st);
+      else if (sc_dt == MK_DT_F16)
+        rc = launch_fast<BITS, bf16, f16, false, NMAT, EPI>(b, gpc, st);
+      else
+        rc = launch_fast<BITS, bf16, float, false, NMAT, EPI>(b, gpc, st);
+    } else {
+      b.M = (int)mrows;
+      if (act_dt == MK_DT_F16 && sc_dt == MK_DT_F16)
+        rc = launch_generic<BITS, f16, f16, NMAT, EPI>(b, (int)gs, st);
+      else if (act_dt == MK_DT_F16)
+        rc = launch_generic<BITS, f16, float, NMAT, EPI>(b, (int)gs, st);
+      else if (sc_dt == MK_DT_F16)
+        rc = launch_generic<BITS, bf16, f16, NMAT, EPI>(b, (int)gs, st);
+      else
+        rc = launch_generic<BITS, bf16, float, NMAT, EPI>(b, (int)gs, st);
+    }
+  }
+  return rc;
+}
+
+template <int BITS>
+int matvec_entry(const void* x, const uint8_t* w, const void* s, const void* z, const void* residual,
+                 void* y_mm, void* y_out, int64_t M, int64_t N, int64_t K, int64_t gs, int act_dt,
+                 int sc_dt, void* stream) {
+  GemvArgs a = {};
+  a.x = x;
+  a.w[0] = a.w[1] = w;
+  a.s[0] = a.s[1] = s;
+  a.z[0] = a.z[1] = z;
+  a.residual = residual;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (residual) {
+    MK_REQUIRE(y_out);
+    a.y0 = y_mm;
+    a.y1 = y_out;
+    return gemv_dispatch<BITS, 1, EPI_RESIDUAL>(a, M, N, K, gs, act_dt, sc_dt, st);
+  }
+  void* y = y_out ? y_out : y_mm;
+  MK_REQUIRE(y);
+  a.y0 = y;
+  int rc = gemv_dispatch<BITS, 1, EPI_NONE>(a, M, N, K, gs, act_dt, sc_dt, st);
+  if (rc == MK_OK && y_mm && y_out && y_mm != y_out) {
+    hipError_t e = hipMemcpyAsync(y_mm, y_out, (size_t)M * N * 2, hipMemcpyDeviceToDevice, st);
+    if (e != hipSuccess) return -(int)e - 1000;
+  }
+  return rc;
+}
+
+template <int BITS>
+int gate_up_entry(const void* x, const uint8_t* wg, const uint8_t* wu, const void* sg,
+                  const void* su, const void* zg, const void* zu, void* gate_out, void* up_out,
+                  void* mlp_out, int64_t M, int64_t N, int64_t K, int64_t gs, int act_dt,
+                  int sc_dt, void* stream) {
+  MK_REQUIRE(gate_out || up_out || mlp_out);
+  GemvArgs a = {};
+  a.x = x;
+  a.w[0] = wg;
+  a.w[1] = wu;
+  a.s[0] = sg;
+  a.s[1] = su;
+  a.z[0] = zg;
+  a.z[1] = zu;
+  a.y0 = gate_out;
+  a.y1 = up_out;
+  a.y2 = mlp_out;
+  return gemv_dispatch<BITS, 2, EPI_GATE_UP>(a, M, N, K, gs, act_dt, sc_dt,
+                                             reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int mk_q4_matvec(const void* x, const uint8_t* w, const void* scales, const void* zeros,
+                 const void* residual, void* y_mm, void* y_out, int64_t M, int64_t N, int64_t K,
+                 int64_t group_size, int act_dtype, int scale_dtype, void* stream) {
+  return matvec_entry<4>(x, w, scales, zeros, residual, y_mm, y_out, M, N, K, group_size, act_dtype,
+                         scale_dtype, stream);
+}
+
+int mk_q8_matvec(const void* x, const uint8_t* w, const void* scales, const void* zeros,
+                 const void* residual, void* y_mm, void* y_out, int64_t M, int64_t N, int64_t K,
+                 int64_t group_size, int act_dtype, int scale_dtype, void* stream) {
+  return matvec_entry<8>(x, w, scales, zeros, residual, y_mm, y_out, M, N, K, group_size, act_dtype,
+                         scale_dtype, stream);
+}
+
+int mk_q4_gate_up(const void* x, const uint8_t* w_gate, const uint8_t* w_up, const void* s_gate,
+                  const void* s_up, const void* z_gate, const void* z_up, void* gate_out,
+                  void* up_out, void* mlp_out, int64_t M, int64_t N, int64_t K,
+                  int64_t group_size, int act_dtype, int scale_dtype, void* stream) {
+  return gate_up_entry<4>(x, w_gate, w_up, s_gate, s_up, z_gate, z_up, gate_out, up_out, mlp_out,
+                          M, N, K, group_size, act_dtype, scale_dtype, stream);
+}
+
+int mk_q8_gate_up(const void* x, const uint8_t* w_gate, const uint8_t* w_up, const void* s_gate,
+                  const void* s_up, const void* z_gate, const void* z_up, void* gate_out,
+                  void* up_out, void* mlp_out, int64_t M, int64_t N, int64_t K,
+                  int64_t group_size, int act_dtype, int scale_dtype, void* stream) {
+  return gate_up_entry<8>(x, w_gate, w_up, s_gate, s_up, z_gate, z_up, gate_out, up_out, mlp_out,
+                          M, N, K, group_size, act_dtype, scale_dtype, stream);
+}
+
+}  // extern "C"

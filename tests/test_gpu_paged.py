@@ -1,0 +1,262 @@
+"""HIP paged KV plumbing and paged decode attention vs the oracle."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import mk.gqa_ops as gqa
+import mk.paged_kv_ops as pk
+import mk.paged_quantized_kv_ops as pq
+from oracle import paged as op
+from tests._data import assert_close, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(seed, B, Hq, Hkv, D, P, mb, lengths=None, dtype=np.float16, extra_pages=3):
+    rng = np.random.default_rng(seed)
+    NP = B * mb + extra_pages
+    Kp = rng.standard_normal((NP, P, Hkv, D)).astype(np.float32)
+    Vp = rng.standard_normal((NP, P, Hkv, D)).astype(np.float32)
+    bt = rng.permutation(NP)[:B * mb].astype(np.int32).reshape(B, mb)
+    q = rng.standard_normal((B, Hq, D)).astype(np.float32)
+    if lengths is None:
+        lengths = rng.integers(1, mb * P + 1, size=B)
+    return q, Kp, Vp, bt, np.asarray(lengths, dtype=np.int32)
+
+
+def _t(a, dev, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dtype).to(dev)
+
+
+# ------------------------------------------------------------ lookup / update
+
+def test_block_table_lookup_bit_exact(dev):
+    for B, MAX_S, P, pos in ((1, 16, 4, 3), (2, 32, 8, [2, 17]), (16, 8192, 16, None)):
+        bt = np.random.default_rng(1).permutation(B * (MAX_S // P)).astype(np.int32).reshape(B, -1)
+        if pos is None:
+            pos = np.random.default_rng(2).integers(0, MAX_S, size=B).tolist()
+        page, off = pk.block_table_lookup(to_dev(bt, dev), pos, P, backend="metal")
+        rp, ro = op.block_table_lookup(bt, np.broadcast_to(np.asarray(pos), (B,)), P)
+        assert np.array_equal(page.cpu().numpy(), rp) and np.array_equal(off.cpu().numpy(), ro)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,MAX_S,P,H,D,pos", [(1, 16, 4, 2, 16, 3), (2, 32, 8, 4, 32, [2, 17]),
+                                               (2, 32, 4, 4, 64, [0, 31]), (16, 8192, 16, 8, 128, None)])
+def test_paged_update_bit_exact(dev, dtype, B, MAX_S, P, H, D, pos):
+    rng = np.random.default_rng(80)
+    NP = B * (MAX_S // P)
+    Kp = _t(rng.standard_normal((NP, P, H, D)), dev, dtype)
+    Vp = _t(rng.standard_normal((NP, P, H, D)), dev, dtype)
+    bt = rng.permutation(NP).astype(np.int32).reshape(B, -1)
+    if pos is None:
+        pos = rng.integers(0, MAX_S, size=B).tolist()
+    k = _t(rng.standard_normal((B, H, D)), dev, dtype)
+    v = _t(rng.standard_normal((B, 1, H, D)), dev, dtype)
+    K0, V0 = Kp.clone(), Vp.clone()
+    K1, V1 = pk.paged_kv_cache_update(Kp, Vp, k, v, to_dev(bt, dev), pos)
+    assert K1 is Kp and V1 is Vp  # in place
+    rK, rV = op.paged_kv_update(K0.float().cpu().numpy(), V0.float().cpu().numpy(), k.float().cpu().numpy(),
+                                v[:, 0].float().cpu().numpy(), bt, np.broadcast_to(np.asarray(pos), (B,)))
+    assert np.array_equal(K1.float().cpu().numpy(), rK) and np.array_equal(V1.float().cpu().numpy(), rV)
+
+
+def test_paged_update_collision_later_b_wins(dev):
+    P, H, D = 4, 2, 8
+    Kp = torch.zeros((4, P, H, D), dtype=torch.float16, device=dev)
+    Vp = torch.zeros_like(Kp)
+    bt = torch.tensor([[1, 2], [1, 3], [0, 3]], dtype=torch.int32, device=dev)
+    k = torch.arange(3, dtype=torch.float16, device=dev).reshape(3, 1, 1).expand(3, H, D).contiguous() + 1
+    pk.paged_kv_cache_update(Kp, Vp, k, k, bt, [2, 2, 6])  # b0, b1 -> (1,2); b2 -> (3,2)
+    assert torch.all(Kp[1, 2] == 2) and torch.all(Kp[3, 2] == 3) and int((Kp != 0).sum()) == 2 * H * D
+
+
+# ------------------------------------------------------------ fp16 paged attention
+
+ATTN_CASES = [
+    # (B, Hq, Hkv, D, P, max_blocks)   fast path D in {64,128}; generic otherwise
+    (2, 4, 4, 64, 4, 8),
+    (2, 4, 2, 128, 8, 6),
+    (3, 4, 1, 64, 16, 5),
+    (2, 32, 8, 128, 16, 40),
+    (1, 8, 8, 128, 16, 300),
+    (2, 64, 2, 64, 16, 20),
+    (2, 4, 2, 16, 4, 8),
+    (2, 2, 1, 96, 8, 6),
+    (1, 3, 3, 17 * 2, 4, 4),
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,P,mb", ATTN_CASES)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_paged_gqa_attention(dev, B, Hq, Hkv, D, P, mb, dtype):
+    q, Kp, Vp, bt, lengths = _case(B * 100 + D + mb, B, Hq, Hkv, D, P, mb)
+    qt, Kt, Vt = _t(q, dev, dtype), _t(Kp, dev, dtype), _t(Vp, dev, dtype)
+    got = gqa.paged_gqa_decode_attention(qt[:, None], Kt, Vt, to_dev(bt, dev), to_dev(lengths, dev))
+    ref = op.paged_attention(qt.float().cpu().numpy(), Kt.float().cpu().numpy(), Vt.float().cpu().numpy(), bt,
+                             lengths)
+    tol = 1e-2 if dtype == torch.float16 else 3e-2
+    assert_close(got[:, 0], ref, rtol=tol, atol=1e-3 if dtype == torch.float16 else 4e-3,
+                 what=f"B{B} Hq{Hq} Hkv{Hkv} D{D} P{P}")
+
+
+def test_paged_attention_edge_lengths(dev):
+    q, Kp, Vp, bt, _ = _case(5, 4, 8, 2, 128, 16, 70)
+    lengths = np.array([0, 1, 17, 70 * 16], np.int32)
+    qt, Kt, Vt = (_t(a, dev, torch.float16) for a in (q, Kp, Vp))
+    got = gqa.paged_gqa_decode_attention(qt[:, None], Kt, Vt, to_dev(bt, dev), to_dev(lengths, dev))[:, 0]
+    assert torch.all(got[0] == 0)
+    first = Kt.new_empty((8, 128))
+    for h in range(8):
+        first[h] = Vt[bt[1, 0], 0, h // 4]
+    assert torch.equal(got[1], first)
+    ref = op.paged_attention(qt.float().cpu().numpy(), Kt.float().cpu().numpy(), Vt.float().cpu().numpy(), bt,
+                             lengths)
+    assert_close(got, ref, what="edge lengths")
+
+
+def test_paged_attention_invalid_pages_skipped(dev):
+    q, Kp, Vp, bt, lengths = _case(6, 2, 4, 2, 64, 8, 6, lengths=[48, 40])
+    bt = bt.copy()
+    bt[0, 2] = -1
+    bt[1, 4] = Kp.shape[0] + 5
+    qt, Kt, Vt = (_t(a, dev, torch.float16) for a in (q, Kp, Vp))
+    got = gqa.paged_gqa_decode_attention(qt[:, None], Kt, Vt, to_dev(bt, dev), to_dev(lengths, dev))[:, 0]
+    ref = op.paged_attention(qt.float().cpu().numpy(), Kt.float().cpu().numpy(), Vt.float().cpu().numpy(), bt,
+                             lengths)
+    assert_close(got, ref, what="invalid pages")
+
+
+@pytest.mark.parametrize("backend", ["metal", "metal_threadgroup", "metal_d64", "auto"])
+def test_paged_decode_attention_mha(dev, backend):
+    q, Kp, Vp, bt, lengths = _case(9, 2, 4, 4, 64, 4, 8)
+    qt, Kt, Vt = (_t(a, dev, torch.float16) for a in (q, Kp, Vp))
+    got = pk.paged_decode_attention(qt[:, None], Kt, Vt, to_dev(bt, dev), lengths.tolist(), backend=backend)
+    ref = op.paged_attention(qt.float().cpu().numpy(), Kt.float().cpu().numpy(), Vt.float().cpu().numpy(), bt,
+                             lengths)
+    assert_close(got[:, 0], ref, what=backend)
+    with pytest.raises(ValueError, match="metal_d128"):
+        pk.paged_decode_attention(qt[:, None], Kt, Vt, to_dev(bt, dev), lengths.tolist(), backend="metal_d128")
+
+
+def test_config3_full_size(dev):
+    """B=16, 32/8 heads, D=128, P=16, lengths U[512,8192],
+    permuted block table -- full size against the oracle."""
+    rng = np.random.default_rng(3)
+    B, Hq, Hkv, D, P, mb = 16, 32, 8, 128, 16, 512
+    lengths = rng.integers(512, 8193, size=B).astype(np.int32)
+    NP = B * mb
+    bt = np.random.default_rng(4).permutation(NP).astype(np.int32).reshape(B, mb)
+    Kt = torch.randn((NP, P, Hkv, D), generator=torch.Generator().manual_seed(6)).to(torch.float16).to(dev)
+    Vt = torch.randn((NP, P, Hkv, D), generator=torch.Generator().manual_seed(7)).to(torch.float16).to(dev)
+    qt = torch.randn((B, Hq, D), generator=torch.Generator().manual_seed(5)).to(torch.float16).to(dev)
+    got = gqa.paged_gqa_decode_attention(qt[:, None], Kt, Vt, to_dev(bt, dev), to_dev(lengths, dev))[:, 0]
+    ref = op.paged_attention(qt.float().cpu().numpy(), Kt.cpu().numpy(), Vt.cpu().numpy(), bt, lengths)
+    assert_close(got, ref, what="config 3")
+
+
+# ------------------------------------------------------------ fused split + RoPE + update
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,Hq,Hkv,D,P,mb", [(2, 4, 2, 16, 4, 4), (4, 32, 8, 128, 16, 8), (3, 8, 8, 64, 16, 3)])
+def test_qkv_rope_update_bit_exact(dev, dtype, B, Hq, Hkv, D, P, mb):
+    rng = np.random.default_rng(50 + D)
+    NP = B * mb
+    Kp = _t(rng.standard_normal((NP, P, Hkv, D)), dev, dtype)
+    Vp = _t(rng.standard_normal((NP, P, Hkv, D)), dev, dtype)
+    bt = rng.permutation(NP).astype(np.int32).reshape(B, mb)
+    pos = rng.integers(0, mb * P, size=B)
+    qkv = _t(rng.standard_normal((B, 1, (Hq + 2 * Hkv) * D)), dev, dtype)
+    cos, sin = op.rope_tables(mb * P, D, 500000.0)
+    K0, V0 = Kp.float().cpu().numpy(), Vp.float().cpu().numpy()
+    out, K1, V1 = gqa.paged_gqa_decode_block_from_qkv(
+        qkv, Kp, Vp, to_dev(bt, dev), torch.from_numpy(cos), torch.from_numpy(sin), to_dev(pos, dev),
+        num_attention_heads=Hq, num_key_value_heads=Hkv, head_dim=D)
+    npdt = np.float16 if dtype == torch.float16 else np.float32
+    x = qkv[:, 0].float().cpu().numpy().astype(npdt)
+    rq, rK, rV = op.qkv_rope_paged_update(x, cos, sin, pos, bt, K0.astype(npdt), V0.astype(npdt), Hq, Hkv, D)
+    if dtype == torch.bfloat16:
+        from oracle.quant import round_bf16
+        rK = round_bf16(op.qkv_rope_paged_update(x, cos, sin, pos, bt, K0, V0, Hq, Hkv, D)[1])
+    assert np.array_equal(K1.float().cpu().numpy(), rK.astype(np.float32))
+    assert np.array_equal(V1.float().cpu().numpy(), rV.astype(np.float32))
+    ref = op.paged_attention(_rope_q(x, cos, sin, pos, Hq, D, dtype), K1.float().cpu().numpy(),
+                             V1.float().cpu().numpy(), bt, pos + 1)
+    assert_close(out[:, 0], ref, rtol=1e-2 if dtype == torch.float16 else 3e-2,
+                 atol=1e-3 if dtype == torch.float16 else 4e-3, what="block attention")
+
+
+def _rope_q(x, cos, sin, pos, Hq, D, dtype):
+    q = x[:, :Hq * D].reshape(x.shape[0], Hq, D).astype(np.float32)
+    c, s = cos[pos][:, None, :], sin[pos][:, None, :]
+    r = op.apply_rope(q, c, s)
+    if dtype == torch.float16:
+        return r.astype(np.float16).astype(np.float32)
+    from oracle.quant import round_bf16
+    return round_bf16(r)
+
+
+# ------------------------------------------------------------ quantized KV
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("B,Hq,Hkv,D,P,mb,g", [(2, 4, 2, 64, 4, 4, 32), (2, 32, 8, 128, 16, 40, 64),
+                                               (2, 32, 8, 64, 16, 40, 64), (2, 4, 1, 16, 4, 4, 16),
+                                               (1, 8, 8, 128, 16, 300, 64)])
+def test_quantized_attention(dev, bits, B, Hq, Hkv, D, P, mb, g):
+    q, Kp, Vp, bt, lengths = _case(70 + D + mb, B, Hq, Hkv, D, P, mb)
+    K16, V16 = Kp.astype(np.float16), Vp.astype(np.float16)
+    kq, vq, ks, vs = op.quantize_pages(K16, V16, g, bits)
+    cache = pq.PagedQuantizedKVCache(k_pages_q=to_dev(kq, dev), v_pages_q=to_dev(vq, dev), k_scales=to_dev(ks, dev),
+                                     v_scales=to_dev(vs, dev), block_table=to_dev(bt, dev),
+                                     lengths=to_dev(lengths, dev), bits=bits, page_size=P, group_size=g,
+                                     original_page_shape=K16.shape)
+    qt = _t(q, dev, torch.float16)
+    got = pq.paged_quantized_kv_gqa_decode_attention(qt[:, None], cache, backend=f"metal_q{bits}")
+    ref = op.quantized_paged_attention(qt.float().cpu().numpy(), kq, vq, ks, vs, bt, lengths, g, bits)
+    assert_close(got[:, 0], ref, what=f"q{bits} D{D}")
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("D,g", [(128, 64), (64, 64), (16, 8)])
+def test_quantize_pages_matches_oracle(dev, bits, D, g):
+    rng = np.random.default_rng(90)
+    K = rng.standard_normal((6, 4, 2, D)).astype(np.float16)
+    V = rng.standard_normal((6, 4, 2, D)).astype(np.float16)
+    bt = np.arange(6, dtype=np.int32).reshape(2, 3)
+    c = pq.quantize_kv_pages(to_dev(K, dev), to_dev(V, dev), to_dev(bt, dev), to_dev(np.array([12, 12]), dev),
+                             pq.PagedQuantizedKVConfig(bits=bits, page_size=4, group_size=g))
+    kq, vq, ks, vs = op.quantize_pages(K, V, g, bits)
+    assert np.array_equal(c.k_pages_q.cpu().numpy(), kq) and np.array_equal(c.v_pages_q.cpu().numpy(), vq)
+    assert np.array_equal(c.k_scales.cpu().numpy(), ks) and np.array_equal(c.v_scales.cpu().numpy(), vs)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("B,Hq,Hkv,D,P,mb,g", [(2, 4, 2, 64, 4, 4, 32), (8, 32, 8, 128, 16, 8, 64),
+                                               (3, 32, 8, 64, 16, 5, 64)])
+def test_quantized_fused_update_bit_exact(dev, bits, B, Hq, Hkv, D, P, mb, g):
+    rng = np.random.default_rng(95 + D)
+    NP = B * mb
+    K16 = rng.standard_normal((NP, P, Hkv, D)).astype(np.float16)
+    kq, vq, ks, vs = op.quantize_pages(K16, K16[::-1].copy(), g, bits)
+    bt = rng.permutation(NP).astype(np.int32).reshape(B, mb)
+    pos = rng.integers(0, mb * P, size=B)
+    qkv = rng.standard_normal((B, 1, (Hq + 2 * Hkv) * D)).astype(np.float16)
+    cos, sin = op.rope_tables(mb * P, D, 500000.0)
+    cache = pq.PagedQuantizedKVCache(k_pages_q=to_dev(kq, dev), v_pages_q=to_dev(vq, dev), k_scales=to_dev(ks, dev),
+                                     v_scales=to_dev(vs, dev), block_table=to_dev(bt, dev),
+                                     lengths=to_dev(pos + 1, dev), bits=bits, page_size=P, group_size=g,
+                                     original_page_shape=K16.shape)
+    q_out, cache = pq.paged_quantized_kv_update_from_qkv(
+        to_dev(qkv, dev), cache, torch.from_numpy(cos), torch.from_numpy(sin), pos.tolist(),
+        num_attention_heads=Hq, num_key_value_heads=Hkv, head_dim=D)
+    rq, rkq, rvq, rks, rvs = op.qkv_rope_paged_update_quant(qkv[:, 0], cos, sin, pos, bt, kq, vq, ks, vs, Hq, Hkv,
+                                                            D, g, bits)
+    assert np.array_equal(q_out[:, 0].cpu().numpy(), rq)
+    assert np.array_equal(cache.k_pages_q.cpu().numpy(), rkq) and np.array_equal(cache.v_pages_q.cpu().numpy(), rvq)
+    assert np.array_equal(cache.k_scales.cpu().numpy(), rks) and np.array_equal(cache.v_scales.cpu().numpy(), rvs)
+    got = pq.paged_quantized_kv_gqa_decode_attention(q_out, cache, backend=f"metal_q{bits}")
+    ref = op.quantized_paged_attention(rq.astype(np.float32), rkq, rvq, rks, rvs, bt, pos + 1, g, bits)
+    assert_close(got[:, 0], ref, what="attention after fused write")

@@ -1,0 +1,197 @@
+"""HIP q4/q8 pack, dequant, matvec, gate/up and MLP block vs the oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+import mk.mlp_block_ops as mlp
+import mk.quant_ops as qo
+from oracle import quant as oq
+from tests._data import assert_close, quant_weight, to_dev
+
+pytestmark = pytest.mark.gpu
+
+ACT = {"f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _x(rng, M, K, act, dev):
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    t = torch.from_numpy(x).to(ACT[act]).to(dev)
+    return t, t.float().cpu().numpy()
+
+
+# ------------------------------------------------------------ bit-exact integer paths
+
+def test_pack_unpack_bit_exact(dev):
+    rng = np.random.default_rng(60)
+    for shape in ((4, 64), (3, 65), (1, 1), (7, 4096)):
+        q = rng.integers(0, 16, size=shape, dtype=np.uint8)
+        got = qo.pack_q4(to_dev(q, dev))
+        assert np.array_equal(got.cpu().numpy(), oq.pack_q4(q))
+        back = qo.unpack_q4(got, shape[1])
+        assert np.array_equal(back.cpu().numpy(), q)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("zeros_kind", ["none", "sym", "affine"])
+@pytest.mark.parametrize("out", ["f16", "bf16"])
+@pytest.mark.parametrize("sdt", [torch.float32, torch.float16])
+def test_dequant_bit_exact(dev, bits, zeros_kind, out, sdt):
+    rng = np.random.default_rng(61)
+    M, K, g = 5, 96, 32
+    codes, stored, s, z = quant_weight(rng, M, K, g, bits, zeros_kind, "normal")
+    s = torch.from_numpy(s).to(sdt).float().numpy()  # the values the kernel will see
+    if z is not None:
+        z = torch.from_numpy(z).to(sdt).float().numpy()
+    fn = qo.dequant_q4 if bits == 4 else qo.dequant_q8
+    got = fn(to_dev(stored, dev), to_dev(s, dev, sdt), to_dev(z, dev, sdt), group_size=g, out_dtype=ACT[out],
+             backend="metal")
+    ref = oq.dequant(codes, s, z, g, np.float32)
+    ref = ref.astype(np.float16).astype(np.float32) if out == "f16" else oq.round_bf16(ref)
+    assert np.array_equal(got.float().cpu().numpy(), ref)
+
+
+# ------------------------------------------------------------ matvec
+
+MATVEC_CASES = [
+    # (M, N, K, g)  -- reference test shapes, generic-path shapes, fast-path shapes
+    (1, 32, 64, 32),
+    (2, 50, 96, 16),
+    (2, 48, 128, 32),
+    (1, 64, 64, 8),
+    (3, 33, 256, 64),
+    (1, 4096, 4096, 64),
+    (4, 1000, 4096, 64),
+    (8, 4096, 14336, 64),
+    (16, 96, 512, 128),
+    (17, 64, 256, 64),
+]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M,N,K,g", MATVEC_CASES)
+def test_matvec_f16(dev, bits, M, N, K, g):
+    rng = np.random.default_rng(100 + M + N + K)
+    codes, stored, s, z = quant_weight(rng, N, K, g, bits, "sym")
+    xt, xf = _x(rng, M, K, "f16", dev)
+    fn = qo.q4_matvec_decode if bits == 4 else qo.q8_matvec_decode
+    got = fn(xt, to_dev(stored, dev), to_dev(s, dev, torch.float16), to_dev(z, dev, torch.float16), group_size=g,
+             backend="metal")
+    s16 = s.astype(np.float16).astype(np.float32)
+    ref = (oq.q4_matvec if bits == 4 else oq.q8_matvec)(xf.astype(np.float16), stored, s16, z, g)
+    assert_close(got, ref, what=f"q{bits} M{M} N{N} K{K} g{g}")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("act", ["f16", "bf16"])
+@pytest.mark.parametrize("zeros_kind", ["none", "affine"])
+@pytest.mark.parametrize("sdt", [torch.float16, torch.float32])
+@pytest.mark.parametrize("M,N,K,g", [(2, 50, 96, 16), (3, 40, 512, 64)])
+def test_matvec_dtypes_and_zeros(dev, bits, act, zeros_kind, sdt, M, N, K, g):
+    rng = np.random.default_rng(7)
+    codes, stored, s, z = quant_weight(rng, N, K, g, bits, zeros_kind, "normal")
+    s = torch.from_numpy(s).to(sdt).float().numpy()
+    z = None if z is None else torch.from_numpy(z).to(sdt).float().numpy()
+    xt, xf = _x(rng, M, K, act, dev)
+    fn = qo.q4_matvec_decode if bits == 4 else qo.q8_matvec_decode
+    got = fn(xt[:, None, :], to_dev(stored, dev), to_dev(s, dev, sdt), to_dev(z, dev, sdt), group_size=g,
+             backend="metal_tiled")
+    ref = (oq.q4_matvec if bits == 4 else oq.q8_matvec)(xf, stored, s, z, g, act=act)
+    assert got.dtype == ACT[act] and tuple(got.shape) == (M, N)
+    assert_close(got, ref, rtol=1e-2 if act == "f16" else 2e-2, what=f"q{bits} {act} {zeros_kind}")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_matvec_saturates(dev, bits):
+    K = 256
+    x = torch.full((1, K), 200.0, dtype=torch.float16, device=dev)
+    codes = np.full((16, K), 15 if bits == 4 else 255, np.uint8)
+    stored = oq.pack_q4(codes) if bits == 4 else codes
+    s = torch.full((16, K // 64), 4.0, dtype=torch.float16, device=dev)
+    fn = qo.q4_matvec_decode if bits == 4 else qo.q8_matvec_decode
+    y = fn(x, to_dev(stored, dev), s, None, group_size=64)
+    assert torch.all(y == 65504.0)
+    y = fn(-x, to_dev(stored, dev), s, None, group_size=64)
+    assert torch.all(y == -65504.0)
+
+
+# ------------------------------------------------------------ gate / up / MLP
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("rows,N,K,g", [(3, 50, 96, 32), (1, 14336, 4096, 64), (8, 512, 4096, 64), (5, 64, 95, 32)])
+def test_gate_up_and_swiglu_epilogue(dev, bits, rows, N, K, g):
+    if bits == 8 and K % 2:
+        pytest.skip("odd K only matters for the q4 ceil(K/2) packing")
+    rng = np.random.default_rng(11 + rows + N)
+    cg, sg_stored, sg, zg = quant_weight(rng, N, K, g, bits, "sym")
+    cu, su_stored, su, zu = quant_weight(rng, N, K, g, bits, "sym")
+    xt, xf = _x(rng, rows, K, "f16", dev)
+    args = (to_dev(sg_stored, dev), to_dev(su_stored, dev), to_dev(sg, dev, torch.float16),
+            to_dev(su, dev, torch.float16), to_dev(zg, dev, torch.float16), to_dev(zu, dev, torch.float16))
+    fn = qo.q4_gate_up_matvec_tiled if bits == 4 else qo.q8_gate_up_matvec_tiled
+    gate, up = fn(xt, *args, group_size=g)
+    mv = oq.q4_matvec if bits == 4 else oq.q8_matvec
+    x16 = xf.astype(np.float16)
+    rg = mv(x16, sg_stored, sg.astype(np.float16).astype(np.float32), zg, g)
+    ru = mv(x16, su_stored, su.astype(np.float16).astype(np.float32), zu, g)
+    assert_close(gate, rg, what="gate")
+    assert_close(up, ru, what="up")
+    mlp_out = qo.q_gate_up_swiglu(xt, args[0], args[1], args[2], args[3], args[4], args[5], bits=bits, group_size=g)
+    # the epilogue consumes the kernel's own rounded gate/up
+    assert_close(mlp_out, oq.swiglu(gate.cpu().numpy(), up.cpu().numpy()), rtol=1e-3, what="swiglu epilogue")
+    assert_close(mlp_out, oq.swiglu(rg, ru), what="swiglu vs oracle")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("preset", ["tiled", "fused_experimental", "parallel", "metal"])
+@pytest.mark.parametrize("B,S,D,I,g", [(1, 1, 64, 128, 32), (2, 1, 64, 130, 32), (1, 1, 4096, 14336, 64),
+                                       (4, 1, 256, 512, 64)])
+def test_mlp_block(dev, bits, preset, B, S, D, I, g):
+    if I % 2 and bits == 4 and preset != "fused_experimental":
+        pytest.skip("q4 matvec backends require even K (ops/quant_ops.py:543)")
+    rng = np.random.default_rng(21 + D + I)
+    x = rng.standard_normal((B, S, D)).astype(np.float16)
+    r = rng.standard_normal((B, S, D)).astype(np.float16)
+    nw = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float16)
+    mats = [quant_weight(rng, I, D, g, bits, "sym"), quant_weight(rng, I, D, g, bits, "sym"),
+            quant_weight(rng, D, I, g, bits, "sym")]
+    dv = lambda m: (to_dev(m[1], dev), to_dev(m[2], dev, torch.float16), to_dev(m[3], dev, torch.float16))
+    (gw, gs, gz), (uw, us, uz), (dw, ds, dz) = dv(mats[0]), dv(mats[1]), dv(mats[2])
+    out, inter = mlp.quantized_mlp_block(
+        to_dev(x, dev), to_dev(r, dev), to_dev(nw, dev), gw, gs, uw, us, dw, ds, gate_zeros=gz, up_zeros=uz,
+        down_zeros=dz, bits=bits, group_size=g, backend_preset=preset, return_intermediates=True)
+    trip = lambda m: (m[1], m[2].astype(np.float16).astype(np.float32), m[3])
+    ref, rint = oq.mlp_block(x.reshape(-1, D), r.reshape(-1, D), nw, trip(mats[0]), trip(mats[1]), trip(mats[2]),
+                             bits=bits, group_size=g, intermediates=True)
+    assert tuple(out.shape) == (B, S, D)
+    assert_close(out.reshape(-1, D), ref, what="mlp out")
+    for k in ("z", "normed", "gate", "up", "mlp", "down"):
+        assert_close(inter[k].reshape(B * S, -1), rint[k], what=k)
+
+
+def test_mlp_decode_step(dev):
+    rng = np.random.default_rng(31)
+    D, I, g = 256, 512, 64
+    x = rng.standard_normal((2, 1, D)).astype(np.float16)
+    nw = np.ones(D, np.float16)
+    mats = [quant_weight(rng, I, D, g, 4, "sym"), quant_weight(rng, I, D, g, 4, "sym"),
+            quant_weight(rng, D, I, g, 4, "sym")]
+    dv = lambda m: (to_dev(m[1], dev), to_dev(m[2], dev, torch.float16))
+    out = mlp.quantized_mlp_decode_step(to_dev(x, dev), to_dev(nw, dev), *dv(mats[0]), *dv(mats[1]), *dv(mats[2]),
+                                        gate_zeros=to_dev(mats[0][3], dev, torch.float16),
+                                        up_zeros=to_dev(mats[1][3], dev, torch.float16),
+                                        down_zeros=to_dev(mats[2][3], dev, torch.float16), bits=4, group_size=g,
+                                        backend_preset="parallel")
+    trip = lambda m: (m[1], m[2].astype(np.float16).astype(np.float32), m[3])
+    ref = oq.mlp_block(x.reshape(-1, D), x.reshape(-1, D), nw, trip(mats[0]), trip(mats[1]), trip(mats[2]), bits=4,
+                       group_size=g)
+    assert_close(out.reshape(-1, D), ref, what="decode step")
+
+
+def test_reference_backend_matches_oracle(dev):
+    rng = np.random.default_rng(41)
+    codes, stored, s, z = quant_weight(rng, 64, 128, 32, 4, "affine", "normal")
+    xt, xf = _x(rng, 2, 128, "f16", dev)
+    got = qo.q4_matvec_decode(xt, to_dev(stored, dev), to_dev(s, dev), to_dev(z, dev), group_size=32,
+                              backend="reference")
+    assert_close(got, oq.q4_matvec(xf.astype(np.float16), stored, s, z, 32), what="reference backend")
