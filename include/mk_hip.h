@@ -160,6 +160,13 @@ int mk_qkv_rope_paged_update_quant(const void* qkv, const float* cos_t, const fl
                                    int64_t num_pages, int64_t cos_rows, int64_t group_size,
                                    int bits, int dtype, void* stream);
 
+/* quantize_kv_pages -- ops/paged_quantized_kv_ops.py:194-292 for one of K or V:
+ * src [rows, D] (rows = num_pages*P*Hkv) -> codes [rows, D] (q8) or
+ * [rows, ceil(D/2)] (q4) and fp16 scales [rows, ceil(D/g)], with the
+ * quantizer of :146-175 (correctly rounded fp32 divide, round half to even). */
+int mk_quantize_kv(const void* src, uint8_t* codes, f16_storage_t* scales, int64_t rows, int64_t D,
+                   int64_t group_size, int bits, int dtype, void* stream);
+
 /* ---------------------------------------------------------------- paged decode attention */
 
 /* Workspace (bytes) the split-K attention kernels need for B sequences of at

@@ -118,6 +118,37 @@ __device__ __forceinline__ u32x4 ldg128_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
+// Hide a constant from the optimizer so it lives in a VGPR: gfx9 VOP3
+// instructions accept at most one scalar/literal operand, and
+// v_and_or_b32(x, mask, magic) needs the magic in a vector register.
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// v_perm_b32: byte i of the result is byte sel[i] of the 8-byte value
+// {hi:src0, lo:src1} (selector values 0-3 pick src1, 4-7 pick src0).
+__device__ __forceinline__ uint32_t perm_b32(uint32_t src0, uint32_t src1, uint32_t sel) {
+  return __builtin_amdgcn_perm(src0, src1, sel);
+}
+// low halves: (lo16(a), lo16(b)) as (low, high) of the result
+__device__ __forceinline__ uint32_t pack_lo16(uint32_t a, uint32_t b) {
+  return perm_b32(b, a, 0x05040100u);
+}
+// high halves: (hi16(a), hi16(b))
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
+  return perm_b32(b, a, 0x07060302u);
+}
+
+// Workgroup barrier for LDS data only.  __syncthreads() is also a global
+// memory fence, for which the compiler waits on every outstanding vector
+// load (vmcnt(0)); here only LDS writes must be complete (lgkmcnt(0)), so
+// weight loads issued earlier stay in flight across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt=63 (no wait), expcnt=7, lgkmcnt=0
+  __builtin_amdgcn_s_barrier();
+}
+
 // ---------------------------------------------------------------------------
 // host-side launch status
 // ---------------------------------------------------------------------------

@@ -71,6 +71,91 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const T* __restrict__ x,
   }
 }
 
+// 8 consecutive elements through 128-bit accesses (16-byte aligned pointers).
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float (&o)[8]) {
+  T t[8];
+  if constexpr (sizeof(T) == 2) {
+    const u32x4 v = ldg128(p);
+    __builtin_memcpy(t, &v, 16);
+  } else {
+    const u32x4 a = ldg128(p), b = ldg128(p + 4);
+    __builtin_memcpy(t, &a, 16);
+    __builtin_memcpy(t + 4, &b, 16);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = to_f32(t[i]);
+}
+
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const T (&t)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    u32x4 v;
+    __builtin_memcpy(&v, t, 16);
+    *reinterpret_cast<u32x4*>(p) = v;
+  } else {
+    u32x4 a, b;
+    __builtin_memcpy(&a, t, 16);
+    __builtin_memcpy(&b, t + 4, 16);
+    reinterpret_cast<u32x4*>(p)[0] = a;
+    reinterpret_cast<u32x4*>(p)[1] = b;
+  }
+}
+
+// Same arithmetic as rms_norm_kernel, for D % 8 == 0 and D <= 8 * 256 * CH:
+// each thread owns CH chunks of 8 elements, loads x, r and w for all of them
+// before the single block reduction, and keeps them in registers (one HBM
+// round trip instead of D / 256 dependent ones).
+template <typename T, typename WT, bool RES, int CH>
+__global__ __launch_bounds__(256) void rms_norm_vec_kernel(const T* __restrict__ x,
+                                                           const T* __restrict__ r,
+                                                           const WT* __restrict__ w,
+                                                           T* __restrict__ z_out,
+                                                           T* __restrict__ y, int64_t D, float eps) {
+  const int64_t row = blockIdx.x;
+  const int nch = (int)(D >> 3);
+  float v[CH][8], wv[CH][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = threadIdx.x + 256 * c;
+    if (ch < nch) {
+      const int64_t off = row * D + 8 * ch;
+      load8(x + off, v[c]);
+      load8(w + 8 * ch, wv[c]);
+      if constexpr (RES) {
+        float rv[8];
+        load8(r + off, rv);
+        T zt[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          zt[i] = from_f32<T>(v[c][i] + rv[i]);
+          v[c][i] = to_f32(zt[i]);
+        }
+        store8(z_out + off, zt);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += v[c][i] * v[c][i];
+    }
+  }
+  __shared__ float part[4];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = part[0] + part[1] + part[2] + part[3];
+  const float inv = rsqrtf(tot / (float)D + eps);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = threadIdx.x + 256 * c;
+    if (ch < nch) {
+      T o[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(v[c][i] * inv * wv[c][i]);
+      store8(y + row * D + 8 * ch, o);
+    }
+  }
+}
+
 inline dim3 grid_for(int64_t work, int threads) {
   int64_t b = (work + threads - 1) / threads;
   if (b > 65536) b = 65536;
@@ -89,9 +174,22 @@ int norm_entry(const void* x, const void* r, const void* w, void* z, void* y, in
   if (rows == 0) return MK_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)rows);
+  // the vector kernel needs 16-byte aligned rows: D % 8 == 0 and aligned bases
+  const bool vec = D % 8 == 0 && D <= 8 * 256 * 4 && mk_aligned(x, 16) && mk_aligned(w, 16) &&
+                   mk_aligned(y, 16) && (!RES || (mk_aligned(r, 16) && mk_aligned(z, 16)));
+  const int ch = (int)((D / 8 + 255) / 256);
+#define MK_NORM_VEC(T, WT, CH)                                                         \
+  rms_norm_vec_kernel<T, WT, RES, CH><<<grid, 256, 0, st>>>((const T*)x, (const T*)r, \
+                                                            (const WT*)w, (T*)z, (T*)y, D, eps)
 #define MK_NORM(T, WT)                                                                       \
-  rms_norm_kernel<T, WT, RES><<<grid, 256, 0, st>>>((const T*)x, (const T*)r, (const WT*)w, \
-                                                    (T*)z, (T*)y, D, eps)
+  do {                                                                                       \
+    if (vec && ch == 1) MK_NORM_VEC(T, WT, 1);                                               \
+    else if (vec && ch == 2) MK_NORM_VEC(T, WT, 2);                                          \
+    else if (vec) MK_NORM_VEC(T, WT, 4);                                                     \
+    else                                                                                     \
+      rms_norm_kernel<T, WT, RES><<<grid, 256, 0, st>>>((const T*)x, (const T*)r,            \
+                                                        (const WT*)w, (T*)z, (T*)y, D, eps); \
+  } while (0)
   if (xdt == MK_DT_F16) {
     if (wdt == MK_DT_F16) MK_NORM(f16, f16);
     else if (wdt == MK_DT_BF16) MK_NORM(f16, bf16);
@@ -106,6 +204,7 @@ int norm_entry(const void* x, const void* r, const void* w, void* z, void* y, in
     else MK_NORM(float, float);
   }
 #undef MK_NORM
+#undef MK_NORM_VEC
   MK_CHECK_LAUNCH();
   return MK_OK;
 }

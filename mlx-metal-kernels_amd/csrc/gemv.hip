@@ -47,18 +47,18 @@ __device__ __forceinline__ u32x4 xperm(u32x4 X) {
   } else if constexpr (BITS == 4) {
     // weight order [0,4,1,5,2,6,3,7]
     u32x4 r;
-    r[0] = (X[0] & 0xFFFFu) | (X[2] << 16);
-    r[1] = (X[0] >> 16) | (X[2] & 0xFFFF0000u);
-    r[2] = (X[1] & 0xFFFFu) | (X[3] << 16);
-    r[3] = (X[1] >> 16) | (X[3] & 0xFFFF0000u);
+    r[0] = pack_lo16(X[0], X[2]);
+    r[1] = pack_hi16(X[0], X[2]);
+    r[2] = pack_lo16(X[1], X[3]);
+    r[3] = pack_hi16(X[1], X[3]);
     return r;
   } else {
     // weight order [0,2,1,3,4,6,5,7]
     u32x4 r;
-    r[0] = (X[0] & 0xFFFFu) | (X[1] << 16);
-    r[1] = (X[0] >> 16) | (X[1] & 0xFFFF0000u);
-    r[2] = (X[2] & 0xFFFFu) | (X[3] << 16);
-    r[3] = (X[2] >> 16) | (X[3] & 0xFFFF0000u);
+    r[0] = pack_lo16(X[0], X[1]);
+    r[1] = pack_hi16(X[0], X[1]);
+    r[2] = pack_lo16(X[2], X[3]);
+    r[3] = pack_hi16(X[2], X[3]);
     return r;
   }
 }
@@ -85,13 +85,14 @@ __device__ __forceinline__ GpMagic make_gp_magic(f16 s, f16 z) {
 }
 
 // q4 word (8 codes) -> 8 fp16 weights in order [0,4,1,5,2,6,3,7].
-__device__ __forceinline__ u32x4 dq4_magic(uint32_t u, const GpMagic& g) {
+// `magic` = 0x64006400 held in a VGPR so each unpack is one v_and_or_b32.
+__device__ __forceinline__ u32x4 dq4_magic(uint32_t u, const GpMagic& g, uint32_t magic) {
   const f16x2 k1024 = {(f16)1024.0f, (f16)1024.0f};
   const uint32_t v = u >> 8;
-  f16x2 a = bitcast<f16x2>((u & 0x000F000Fu) | 0x64006400u) - k1024;  // c0, c4
-  f16x2 b = bitcast<f16x2>((u & 0x00F000F0u) | 0x64006400u) - k1024;  // 16*c1, 16*c5
-  f16x2 c = bitcast<f16x2>((v & 0x000F000Fu) | 0x64006400u) - k1024;  // c2, c6
-  f16x2 d = bitcast<f16x2>((v & 0x00F000F0u) | 0x64006400u) - k1024;  // 16*c3, 16*c7
+  f16x2 a = bitcast<f16x2>((u & 0x000F000Fu) | magic) - k1024;  // c0, c4
+  f16x2 b = bitcast<f16x2>((u & 0x00F000F0u) | magic) - k1024;  // 16*c1, 16*c5
+  f16x2 c = bitcast<f16x2>((v & 0x000F000Fu) | magic) - k1024;  // c2, c6
+  f16x2 d = bitcast<f16x2>((v & 0x00F000F0u) | magic) - k1024;  // 16*c3, 16*c7
   a = __builtin_elementwise_fma(a, g.s, g.nzs);
   b = __builtin_elementwise_fma(b, g.s16, g.nzs);
   c = __builtin_elementwise_fma(c, g.s, g.nzs);
@@ -104,13 +105,24 @@ __device__ __forceinline__ u32x4 dq4_magic(uint32_t u, const GpMagic& g) {
   return r;
 }
 
+// byte-pair unpack of q8 codes with v_perm_b32: bytes (b0, 0x64, b2, 0x64)
+// and (b1, 0x64, b3, 0x64) of {magic8 = 0x64646464, u} are 1024+b0 / 1024+b2
+// and 1024+b1 / 1024+b3 as fp16 pairs.
+__device__ __forceinline__ uint32_t q8_lo_pair(uint32_t u, uint32_t magic8) {
+  return perm_b32(magic8, u, 0x04020400u);
+}
+__device__ __forceinline__ uint32_t q8_hi_pair(uint32_t u, uint32_t magic8) {
+  return perm_b32(magic8, u, 0x04030401u);
+}
+
 // two q8 words (8 codes) -> 8 fp16 weights in order [0,2,1,3,4,6,5,7].
-__device__ __forceinline__ u32x4 dq8_magic(uint32_t u0, uint32_t u1, const GpMagic& g) {
+__device__ __forceinline__ u32x4 dq8_magic(uint32_t u0, uint32_t u1, const GpMagic& g,
+                                           uint32_t magic8) {
   const f16x2 k1024 = {(f16)1024.0f, (f16)1024.0f};
-  f16x2 a0 = bitcast<f16x2>((u0 & 0x00FF00FFu) | 0x64006400u) - k1024;
-  f16x2 b0 = bitcast<f16x2>(((u0 >> 8) & 0x00FF00FFu) | 0x64006400u) - k1024;
-  f16x2 a1 = bitcast<f16x2>((u1 & 0x00FF00FFu) | 0x64006400u) - k1024;
-  f16x2 b1 = bitcast<f16x2>(((u1 >> 8) & 0x00FF00FFu) | 0x64006400u) - k1024;
+  f16x2 a0 = bitcast<f16x2>(q8_lo_pair(u0, magic8)) - k1024;
+  f16x2 b0 = bitcast<f16x2>(q8_hi_pair(u0, magic8)) - k1024;
+  f16x2 a1 = bitcast<f16x2>(q8_lo_pair(u1, magic8)) - k1024;
+  f16x2 b1 = bitcast<f16x2>(q8_hi_pair(u1, magic8)) - k1024;
   a0 = __builtin_elementwise_fma(a0, g.s, g.nzs);
   b0 = __builtin_elementwise_fma(b0, g.s, g.nzs);
   a1 = __builtin_elementwise_fma(a1, g.s, g.nzs);
@@ -189,8 +201,40 @@ struct GemvArgs {
 };
 
 // --------------------------------------------------------------------------
-// fast MFMA kernel
+// shared epilogue: value(s) of output row n for activation row m
 // --------------------------------------------------------------------------
+template <typename AT, int EPI>
+__device__ __forceinline__ void store_out(const GemvArgs& args, size_t o, float v0, float v1) {
+  if constexpr (EPI == EPI_NONE) {
+    reinterpret_cast<AT*>(args.y0)[o] = saturate_cast<AT>(v0);
+  } else if constexpr (EPI == EPI_RESIDUAL) {
+    const AT d = saturate_cast<AT>(v0);
+    if (args.y0) reinterpret_cast<AT*>(args.y0)[o] = d;
+    const float r = to_f32(reinterpret_cast<const AT*>(args.residual)[o]);
+    reinterpret_cast<AT*>(args.y1)[o] = from_f32<AT>(r + to_f32(d));
+  } else {
+    const AT g = saturate_cast<AT>(v0);
+    const AT u = saturate_cast<AT>(v1);
+    if (args.y0) reinterpret_cast<AT*>(args.y0)[o] = g;
+    if (args.y1) reinterpret_cast<AT*>(args.y1)[o] = u;
+    if (args.y2) {
+      const float gf = to_f32(g);
+      const float sil = gf / (1.0f + expf(-gf));
+      reinterpret_cast<AT*>(args.y2)[o] = from_f32<AT>(sil * to_f32(u));
+    }
+  }
+}
+
+// --------------------------------------------------------------------------
+// fast MFMA kernel (any M <= 16)
+// --------------------------------------------------------------------------
+template <int BITS, typename ST, int NMAT, int GPC>
+struct WFrag {
+  u32x4 w[NMAT][2];
+  ST s[NMAT][GPC];
+  ST z[NMAT][GPC];
+};
+
 template <int BITS, typename AT, typename ST, bool MAGIC, int GPC, int NMAT, int EPI>
 __global__ __launch_bounds__(512) void gemv_mfma_kernel(const GemvArgs args) {
   using F = QFmt<BITS>;
@@ -209,6 +253,7 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(const GemvArgs args) {
   const int n_ld = n < N ? n : N - 1;  // rows past N load a valid row; results discarded
   const int m = lane & 15;
   const bool x_active = m < M;
+  const uint32_t magic = in_vgpr(BITS == 4 ? 0x64006400u : 0x64646464u);
 
   // this wave's chunk range
   const int chunks = (K + F::KC - 1) / F::KC;
@@ -226,84 +271,82 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(const GemvArgs args) {
   }
   const AT* xrow = reinterpret_cast<const AT*>(args.x) + (size_t)(x_active ? m : 0) * K + kb * F::KL;
 
-  f32x4 acc[NMAT];
-#pragma unroll
-  for (int t = 0; t < NMAT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  for (int c = c_begin; c < c_end; ++c) {
-    const int k0 = c * F::KC + kb * F::KL;  // first k of this lane's chunk
-    const bool valid = k0 < K;
-
-    // ---- loads (issued together so they are in flight at once)
-    u32x4 wv[NMAT][2];
-    u32x4 xv[STEPS];
-    ST sv[NMAT][GPC], zv[NMAT][GPC];
-    if (valid) {
+  // weights and scales of chunk c (the HBM streams); zero past K
+  auto load_w = [&](int c, WFrag<BITS, ST, NMAT, GPC>& f) {
+    const int k0 = c * F::KC + kb * F::KL;
+    if (c < c_end && k0 < K) {
       const size_t boff = (size_t)c * (F::KC * BITS / 8);
-#pragma unroll
-      for (int t = 0; t < NMAT; ++t) {
-        wv[t][0] = ldg128_stream(wrow[t] + boff);
-        wv[t][1] = ldg128_stream(wrow[t] + boff + 16);
-      }
       const int g0 = k0 >> args.lg;
 #pragma unroll
       for (int t = 0; t < NMAT; ++t) {
+        f.w[t][0] = ldg128_stream(wrow[t] + boff);
+        f.w[t][1] = ldg128_stream(wrow[t] + boff + 16);
 #pragma unroll
         for (int j = 0; j < GPC; ++j) {
-          sv[t][j] = srow[t][g0 + j];
-          zv[t][j] = zrow[t] ? zrow[t][g0 + j] : (ST)0.0f;
+          f.s[t][j] = srow[t][g0 + j];
+          f.z[t][j] = zrow[t] ? zrow[t][g0 + j] : (ST)0.0f;
         }
-      }
-      if (x_active) {
-#pragma unroll
-        for (int s = 0; s < STEPS; ++s) xv[s] = ldg128(xrow + (size_t)c * F::KC + 8 * s);
-      } else {
-#pragma unroll
-        for (int s = 0; s < STEPS; ++s) xv[s] = (u32x4){0u, 0u, 0u, 0u};
       }
     } else {
 #pragma unroll
       for (int t = 0; t < NMAT; ++t) {
-        wv[t][0] = (u32x4){0u, 0u, 0u, 0u};
-        wv[t][1] = (u32x4){0u, 0u, 0u, 0u};
+        f.w[t][0] = (u32x4){0u, 0u, 0u, 0u};
+        f.w[t][1] = (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
         for (int j = 0; j < GPC; ++j) {
-          sv[t][j] = (ST)0.0f;
-          zv[t][j] = (ST)0.0f;
+          f.s[t][j] = (ST)0.0f;
+          f.z[t][j] = (ST)0.0f;
         }
       }
+    }
+  };
+
+  f32x4 acc[NMAT];
+#pragma unroll
+  for (int t = 0; t < NMAT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  WFrag<BITS, ST, NMAT, GPC> cur, nxt;
+  load_w(c_begin, cur);
+  for (int c = c_begin; c < c_end; ++c) {
+    load_w(c + 1, nxt);  // prefetch: next chunk's weights are in flight while this one computes
+    const int k0 = c * F::KC + kb * F::KL;
+    u32x4 xv[STEPS];
+    if (x_active && k0 < K) {
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s) xv[s] = ldg128(xrow + (size_t)c * F::KC + 8 * s);
+    } else {
 #pragma unroll
       for (int s = 0; s < STEPS; ++s) xv[s] = (u32x4){0u, 0u, 0u, 0u};
     }
 
-    // ---- dequant + MFMA
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      const u32x4 b = xperm<BITS, MAGIC>(xv[s]);
-      const int j = s / SPG;
+    for (int t = 0; t < NMAT; ++t) {
 #pragma unroll
-      for (int t = 0; t < NMAT; ++t) {
-        u32x4 a;
+      for (int j = 0; j < GPC; ++j) {
         if constexpr (MAGIC) {
-          const GpMagic gp = make_gp_magic((f16)sv[t][j], (f16)zv[t][j]);
-          if constexpr (BITS == 4) {
-            a = dq4_magic(wv[t][s >> 2][s & 3], gp);
-          } else {
-            a = dq8_magic(wv[t][s >> 1][(2 * s) & 3], wv[t][s >> 1][(2 * s + 1) & 3], gp);
+          const GpMagic gp = make_gp_magic((f16)cur.s[t][j], (f16)cur.z[t][j]);
+#pragma unroll
+          for (int s = j * SPG; s < (j + 1) * SPG; ++s) {
+            u32x4 a;
+            if constexpr (BITS == 4) a = dq4_magic(cur.w[t][s >> 2][s & 3], gp, magic);
+            else a = dq8_magic(cur.w[t][s >> 1][(2 * s) & 3], cur.w[t][s >> 1][(2 * s + 1) & 3], gp, magic);
+            acc[t] = mfma_k32<AT>(a, xperm<BITS, MAGIC>(xv[s]), acc[t]);
           }
         } else {
           GpExact gp;
-          gp.s = to_f32(sv[t][j]);
-          gp.z = to_f32(zv[t][j]);
-          if constexpr (BITS == 4) {
-            a = dq4_exact<AT>(wv[t][s >> 2][s & 3], gp);
-          } else {
-            a = dq8_exact<AT>(wv[t][s >> 1][(2 * s) & 3], wv[t][s >> 1][(2 * s + 1) & 3], gp);
+          gp.s = to_f32(cur.s[t][j]);
+          gp.z = to_f32(cur.z[t][j]);
+#pragma unroll
+          for (int s = j * SPG; s < (j + 1) * SPG; ++s) {
+            u32x4 a;
+            if constexpr (BITS == 4) a = dq4_exact<AT>(cur.w[t][s >> 2][s & 3], gp);
+            else a = dq8_exact<AT>(cur.w[t][s >> 1][(2 * s) & 3], cur.w[t][s >> 1][(2 * s + 1) & 3], gp);
+            acc[t] = mfma_k32<AT>(a, xv[s], acc[t]);
           }
         }
-        acc[t] = mfma_k32<AT>(a, b, acc[t]);
       }
     }
+    cur = nxt;
   }
 
   // ---- cross-wave reduction through LDS
@@ -326,26 +369,253 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(const GemvArgs args) {
   for (int i = 0; i < 4; ++i) {
     const int nn = nb + i;
     if (nn >= N) break;
-    const size_t o = (size_t)m * N + nn;
-    if constexpr (EPI == EPI_NONE) {
-      reinterpret_cast<AT*>(args.y0)[o] = saturate_cast<AT>(acc[0][i]);
-    } else if constexpr (EPI == EPI_RESIDUAL) {
-      const AT d = saturate_cast<AT>(acc[0][i]);
-      if (args.y0) reinterpret_cast<AT*>(args.y0)[o] = d;
-      const float r = to_f32(reinterpret_cast<const AT*>(args.residual)[o]);
-      reinterpret_cast<AT*>(args.y1)[o] = from_f32<AT>(r + to_f32(d));
-    } else {
-      const AT g = saturate_cast<AT>(acc[0][i]);
-      const AT u = saturate_cast<AT>(acc[1][i]);
-      if (args.y0) reinterpret_cast<AT*>(args.y0)[o] = g;
-      if (args.y1) reinterpret_cast<AT*>(args.y1)[o] = u;
-      if (args.y2) {
-        const float gf = to_f32(g);
-        const float sil = gf / (1.0f + expf(-gf));
-        reinterpret_cast<AT*>(args.y2)[o] = from_f32<AT>(sil * to_f32(u));
+    store_out<AT, EPI>(args, (size_t)m * N + nn, acc[0][i], acc[NMAT - 1][i]);
+  }
+}
+
+// --------------------------------------------------------------------------
+// M = 1 kernel: v_dot2_f32_f16 on (nearly) raw codes.
+//
+// A lane handles 32-k "units" (16 code bytes for q4, 32 for q8) of R output
+// rows (x NMAT matrices); the R rows share the lane's x registers.  The codes
+// are never scaled: the exponent-magic trick turns each code pair into an
+// fp16 pair, v_dot2 accumulates x . code in fp32, and the group's affine map
+// is applied once per unit in fp32:
+//   sum_k x_k (c_k - z) s = s * (t - B - z * X),   X = sum of x.
+// q4 low nibbles become exact codes c (1024 + c, minus 1024); high nibbles
+// stay 1024 + 16c against x/16, i.e. c + 64 per unit of x, so B = 64 * X_hi
+// (X_hi = sum of the x's met by high nibbles).  q8 bytes are 1024 + c with
+// B = 1024 * X.  Keeping the offset small next to (c - z) keeps the fp32
+// cancellation in (t - B) harmless.  Scales and zero points of the
+// workgroup's rows are staged in LDS.  Needs fp16 activations, fp16 scales,
+// power-of-two group size >= 32, K % 32 == 0.
+// --------------------------------------------------------------------------
+// rows per workgroup (per matrix): 8, except q8 gate/up whose 32 code loads
+// per lane would not fit 4 waves/SIMD worth of registers
+template <int BITS, int NMAT>
+constexpr int dot_rows() {
+  return (BITS == 8 && NMAT == 2) ? 4 : 8;
+}
+constexpr int DOT_SZ_VEC = 2;  // 16-byte (s|z) vectors staged per lane
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(bitcast<f16x2>(a), bitcast<f16x2>(b), c, false);
+}
+
+// Butterfly that halves the live values per step: at distance d a lane keeps
+// the half selected by (lane & d) and adds the partner's copy of it.  After
+// log2(CNT) steps every lane holds one value, then plain butterflies finish
+// the 64-lane sum.  Lane l ends with the total of value index idx(l), where
+// idx adds CNT/2, CNT/4, ... for each set bit 32, 16, ... of l.
+template <int CNT, int D>
+__device__ __forceinline__ void reduce_scatter(float* v, int lane) {
+  if constexpr (D >= 1) {
+    if constexpr (CNT > 1) {
+      constexpr int H = CNT / 2;
+      const bool upper = (lane & D) != 0;
+#pragma unroll
+      for (int j = 0; j < H; ++j) {
+        const float keep = upper ? v[j + H] : v[j];
+        const float send = upper ? v[j] : v[j + H];
+        v[j] = keep + __shfl_xor(send, D, 64);
       }
+      reduce_scatter<H, D / 2>(v, lane);
+    } else {
+      v[0] += __shfl_xor(v[0], D, 64);
+      reduce_scatter<1, D / 2>(v, lane);
     }
   }
+}
+
+template <int BITS, int NMAT, int R>
+struct DotFrag {
+  u32x4 w[NMAT][R][BITS == 4 ? 1 : 2];
+  u32x4 x[4];
+};
+
+template <int BITS, int NMAT, int EPI>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void gemv_dot_kernel(
+    const GemvArgs args) {
+  constexpr int R = dot_rows<BITS, NMAT>();
+  constexpr int V = NMAT * R;  // values reduced per lane
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int kw = args.kw;
+  const int N = args.N, K = args.K, G = args.G;
+  const int n0 = blockIdx.x * R;
+  const uint32_t magic = in_vgpr(BITS == 4 ? 0x64006400u : 0x64646464u);
+  const f16* x = reinterpret_cast<const f16*>(args.x);
+
+  const uint8_t* wrow[NMAT][R];
+#pragma unroll
+  for (int t = 0; t < NMAT; ++t)
+#pragma unroll
+    for (int r = 0; r < R; ++r) wrow[t][r] = args.w[t] + (size_t)min(n0 + r, N - 1) * args.row_bytes;
+
+  // unit u = it * 64 * kw + wave * 64 + lane: one 128-bit code load per row
+  // (two for q8) and four for x; a wave's 64 units are contiguous in k
+  const int U = K / 32;
+  // branch-free: a lane past the last unit re-reads unit 0 (its sums are
+  // dropped), so all loads sit in one block and vmcnt waits stay exact
+  auto load = [&](int u, DotFrag<BITS, NMAT, R>& f) {
+    const int k0 = (u < U ? u : 0) * 32;
+#pragma unroll
+    for (int t = 0; t < NMAT; ++t)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint8_t* p = wrow[t][r] + (uint32_t)(k0 * BITS / 8);
+        f.w[t][r][0] = ldg128_stream(p);
+        if constexpr (BITS == 8) f.w[t][r][BITS == 4 ? 0 : 1] = ldg128_stream(p + 16);
+      }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.x[j] = ldg128(x + k0 + 8 * j);
+  };
+
+  // Scales and zero points: each wave stages, in its own LDS region, the
+  // (s, z) of its rows for the groups its 64 units cover -- NMAT*R*2
+  // contiguous runs of gpw fp16 values, fetched with 128-bit loads.  They are
+  // requested first, then the code loads go out, then the LDS writes (vmcnt is
+  // in order: the writes wait for the small loads only, the code loads stay in
+  // flight).  No workgroup barrier is needed: LDS ops of a wave run in order.
+  const int gpw = 2048 >> args.lg;  // groups per 64-unit slice
+  const int nseg = NMAT * R * 2;    // (matrix, row, s|z) runs
+  const int seg_vec = gpw / 8;      // 16-byte vectors per run
+  const int nvec = nseg * seg_vec;  // <= 64 * DOT_SZ_VEC
+  __shared__ u32x4 szw[8][64 * DOT_SZ_VEC];
+  u32x4 szv[DOT_SZ_VEC];
+  bool sz_zero[DOT_SZ_VEC];
+  int ubase = wave * 64;
+  {
+    // branch-free: lanes without a run (or a missing zero tensor) read a valid
+    // dummy vector and drop it, so every load counts in order for vmcnt
+    const int g0 = (ubase * 32) >> args.lg;
+    const f16* s0 = reinterpret_cast<const f16*>(args.s[0]);
+    const f16* s1 = reinterpret_cast<const f16*>(args.s[NMAT - 1]);
+    const f16* z0 = args.z[0] ? reinterpret_cast<const f16*>(args.z[0]) : s0;
+    const f16* z1 = args.z[NMAT - 1] ? reinterpret_cast<const f16*>(args.z[NMAT - 1]) : s1;
+    const bool has_z = args.z[0] != nullptr;
+#pragma unroll
+    for (int j = 0; j < DOT_SZ_VEC; ++j) {
+      const int v = lane + 64 * j;
+      const bool use = v < nvec && ubase < U;
+      const int seg = use ? v / seg_vec : 0;
+      const int e = use ? v - seg * seg_vec : 0;
+      const int t = seg / (2 * R), r = (seg >> 1) % R, isz = seg & 1;
+      const f16* base = t == 0 ? (isz ? z0 : s0) : (isz ? z1 : s1);
+      const int nr = min(n0 + r, N - 1);
+      szv[j] = ldg128(base + (size_t)nr * G + g0 + 8 * e);
+      sz_zero[j] = isz && !has_z;  // zero tensor absent: z = 0 (applied at the LDS write)
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep the small loads ahead of the code loads
+  DotFrag<BITS, NMAT, R> f;
+  load(ubase + lane, f);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < DOT_SZ_VEC; ++j)
+    szw[wave][lane + 64 * j] = sz_zero[j] ? (u32x4){0u, 0u, 0u, 0u} : szv[j];
+  __builtin_amdgcn_wave_barrier();
+  const f16* szl = reinterpret_cast<const f16*>(&szw[wave][0]);
+
+  float acc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+
+  {  // one 64-unit slice per wave (the dispatcher guarantees U <= 64 * kw)
+    const int u = ubase + lane;
+    const bool valid = u < U;
+    const int k0 = valid ? u * 32 : 0;
+
+    // activation operands in the unpack order, and their sums
+    uint32_t xp[16];
+    float xs_hi = 0.0f, xs = 0.0f;  // X_hi and X
+    const uint32_t one2 = 0x3C003C00u;  // (1.0h, 1.0h)
+    if constexpr (BITS == 4) {
+      const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // word j covers x[8j .. 8j+8): pairs (0,4) (1,5)/16 (2,6) (3,7)/16
+        const uint32_t p0 = pack_lo16(f.x[j][0], f.x[j][2]);
+        const uint32_t p1 = pack_hi16(f.x[j][0], f.x[j][2]);
+        const uint32_t p2 = pack_lo16(f.x[j][1], f.x[j][3]);
+        const uint32_t p3 = pack_hi16(f.x[j][1], f.x[j][3]);
+        xs_hi = dot2(p1, one2, dot2(p3, one2, xs_hi));
+        xs = dot2(p0, one2, dot2(p2, one2, xs));
+        xp[4 * j + 0] = p0;
+        xp[4 * j + 1] = bitcast<uint32_t>(bitcast<f16x2>(p1) * sixteenth);
+        xp[4 * j + 2] = p2;
+        xp[4 * j + 3] = bitcast<uint32_t>(bitcast<f16x2>(p3) * sixteenth);
+      }
+      xs += xs_hi;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // two words per 8 x's: pairs (0,2) (1,3) (4,6) (5,7)
+        xp[4 * j + 0] = pack_lo16(f.x[j][0], f.x[j][1]);
+        xp[4 * j + 1] = pack_hi16(f.x[j][0], f.x[j][1]);
+        xp[4 * j + 2] = pack_lo16(f.x[j][2], f.x[j][3]);
+        xp[4 * j + 3] = pack_hi16(f.x[j][2], f.x[j][3]);
+        xs = dot2(xp[4 * j + 0], one2, dot2(xp[4 * j + 1], one2,
+                  dot2(xp[4 * j + 2], one2, dot2(xp[4 * j + 3], one2, xs))));
+      }
+    }
+    const float boff = BITS == 4 ? 64.0f * xs_hi : 1024.0f * xs;
+    const int gl = (lane * 32) >> args.lg;  // group within this wave's slice
+
+#pragma unroll
+    for (int t = 0; t < NMAT; ++t)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float tsum = 0.0f;
+        if constexpr (BITS == 4) {
+          const f16x2 k1024 = {(f16)1024.0f, (f16)1024.0f};
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const uint32_t q = f.w[t][r][0][w];
+            const uint32_t v = q >> 8;
+            const uint32_t c04 = bitcast<uint32_t>(bitcast<f16x2>((q & 0x000F000Fu) | magic) - k1024);
+            const uint32_t c26 = bitcast<uint32_t>(bitcast<f16x2>((v & 0x000F000Fu) | magic) - k1024);
+            tsum = dot2(c04, xp[4 * w + 0], tsum);
+            tsum = dot2((q & 0x00F000F0u) | magic, xp[4 * w + 1], tsum);
+            tsum = dot2(c26, xp[4 * w + 2], tsum);
+            tsum = dot2((v & 0x00F000F0u) | magic, xp[4 * w + 3], tsum);
+          }
+        } else {
+#pragma unroll
+          for (int w = 0; w < 8; ++w) {
+            const uint32_t q = f.w[t][r][w >> 2][w & 3];
+            tsum = dot2(q8_lo_pair(q, magic), xp[2 * w + 0], tsum);
+            tsum = dot2(q8_hi_pair(q, magic), xp[2 * w + 1], tsum);
+          }
+        }
+        const int seg = (t * R + r) * 2;
+        const float sv = (float)szl[seg * gpw + gl];
+        const float zv = (float)szl[(seg + 1) * gpw + gl];
+        const float term = sv * (tsum - boff - zv * xs);
+        acc[t * R + r] += valid ? term : 0.0f;
+      }
+
+  }
+
+  // ---- 64-lane reduction (halving butterfly), then across waves in LDS
+  reduce_scatter<V, 32>(acc, lane);
+  const float tot = acc[0];
+  int idx = 0;
+#pragma unroll
+  for (int d = 32, h = V / 2; h >= 1; d >>= 1, h >>= 1)
+    if (lane & d) idx += h;
+  __shared__ float red[8][V];
+  constexpr int QUAD = 64 / V;  // lanes holding the same index
+  if ((lane & (QUAD - 1)) == 0) red[wave][idx] = tot;
+  __syncthreads();
+  if (wave != 0 || lane >= R) return;
+  float v0 = 0.0f, v1 = 0.0f;
+  for (int w = 0; w < kw; ++w) {
+    v0 += red[w][lane];
+    if constexpr (NMAT == 2) v1 += red[w][R + lane];
+  }
+  const int nn = n0 + lane;
+  if (nn < N) store_out<f16, EPI>(args, (size_t)nn, v0, v1);
 }
 
 // --------------------------------------------------------------------------
@@ -432,6 +702,15 @@ int launch_fast(const GemvArgs& a, int gpc, hipStream_t st) {
   return MK_OK;
 }
 
+template <int BITS, int NMAT, int EPI>
+int launch_dot(const GemvArgs& a, hipStream_t st) {
+  constexpr int R = dot_rows<BITS, NMAT>();
+  const dim3 grid((a.N + R - 1) / R);
+  gemv_dot_kernel<BITS, NMAT, EPI><<<grid, dim3(64 * a.kw), 0, st>>>(a);
+  MK_CHECK_LAUNCH();
+  return MK_OK;
+}
+
 template <int BITS, typename AT, typename ST, int NMAT, int EPI>
 int launch_generic(const GemvArgs& a, int gs, hipStream_t st) {
   const dim3 grid((a.N + 3) / 4);
@@ -491,7 +770,23 @@ int gemv_dispatch(GemvArgs a, int64_t M, int64_t N, int64_t K, int64_t gs, int a
     if (a.y0) b.y0 = (char*)a.y0 + (size_t)m0 * N * xe;
     if (a.y1) b.y1 = (char*)a.y1 + (size_t)m0 * N * xe;
     if (a.y2) b.y2 = (char*)a.y2 + (size_t)m0 * N * xe;
-    if (fast) {
+    // dot kernel: one 64-unit (2048-k) slice per wave, <= 8 waves; the
+    // (s, z) runs of a slice must be whole 16-byte vectors and fit the stage
+    const int64_t gpw = lg >= 0 ? (2048 >> lg) : 0;
+    const bool dot_ok = fast && mrows == 1 && act_dt == MK_DT_F16 && sc_dt == MK_DT_F16 &&
+                        lg >= 5 && lg <= 8 && (K % 32) == 0 && K <= 8 * 2048 &&
+                        (a.G % 8) == 0 && (gpw % 8) == 0 &&
+                        (int64_t)NMAT * dot_rows<BITS, NMAT>() * 2 * (gpw / 8) <= 64 * DOT_SZ_VEC &&
+                        mk_aligned(a.s[0], 16) && mk_aligned(a.s[NMAT - 1], 16) &&
+                        (a.z[0] == nullptr || (mk_aligned(a.z[0], 16) && mk_aligned(a.z[NMAT - 1], 16)));
+    if (dot_ok) {
+      // one 64-unit slice per wave when K allows (K <= 16384), else loop
+      const int64_t units = K / 32;
+      int64_t kwd = (units + 63) / 64;
+      kwd = kwd < 1 ? 1 : (kwd > 8 ? 8 : kwd);
+      b.kw = (int)kwd;
+      rc = launch_dot<BITS, NMAT, EPI>(b, st);
+    } else if (fast) {
       b.kw = choose_kw(N, K, F::KC);
       if (act_dt == MK_DT_F16 && sc_dt == MK_DT_F16)
         rc = launch_fast<BITS, f16, f16, true, NMAT, EPI>(b, gpc, st);

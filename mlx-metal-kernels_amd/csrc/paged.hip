@@ -216,9 +216,75 @@ __global__ __launch_bounds__(256) void qkv_rope_update_quant_kernel(
   }
 }
 
+// Bulk symmetric quantization of KV rows (every page, slot and kv head):
+// ops/paged_quantized_kv_ops.py:194-292 applied to rows of D values.  One
+// thread per row walks its groups; q4 codes are packed as they are produced,
+// pairs straddling a group boundary included.
+template <typename T, int BITS>
+__global__ void quantize_kv_rows_kernel(const T* __restrict__ src, uint8_t* __restrict__ codes,
+                                        uint16_t* __restrict__ scales, int64_t rows, int D,
+                                        int gs) {
+  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float qmax = BITS == 8 ? 127.0f : 7.0f;
+  const float qoff = BITS == 8 ? 128.0f : 8.0f;
+  const int G = (D + gs - 1) / gs;
+  const T* row = src + r * D;
+  uint8_t* out = codes + r * (BITS == 8 ? D : (D + 1) / 2);
+  uint16_t* srow = scales + r * G;
+  uint32_t pending = 0;
+  for (int g = 0; g < G; ++g) {
+    const int e0 = g * gs, e1 = min(e0 + gs, D);
+    float amax = 0.0f;
+    for (int e = e0; e < e1; ++e) amax = fmaxf(amax, fabsf(to_f32(row[e])));
+    amax = fmaxf(amax, 1e-8f);
+    const float scale = amax / qmax;  // correctly rounded fp32 division
+    srow[g] = bitcast<uint16_t>((f16)scale);
+    for (int e = e0; e < e1; ++e) {
+      float qv = rintf(to_f32(row[e]) / scale);
+      qv = fminf(fmaxf(qv, -qmax), qmax);
+      const uint32_t c = (uint32_t)(int)(qv + qoff);
+      if constexpr (BITS == 8) {
+        out[e] = (uint8_t)c;
+      } else if (e & 1) {
+        out[e >> 1] = (uint8_t)(pending | (c << 4));
+      } else {
+        pending = c;
+      }
+    }
+  }
+  if constexpr (BITS == 4) {
+    if (D & 1) out[D >> 1] = (uint8_t)pending;
+  }
+}
+
 }  // namespace
 
 extern "C" {
+
+int mk_quantize_kv(const void* src, uint8_t* codes, f16_storage_t* scales, int64_t rows, int64_t D,
+                   int64_t group_size, int bits, int dtype, void* stream) {
+  MK_REQUIRE(src && codes && scales && rows >= 0 && D > 0 && group_size > 0);
+  MK_REQUIRE(bits == 4 || bits == 8);
+  MK_REQUIRE(dtype == MK_DT_F16 || dtype == MK_DT_BF16);
+  MK_REQUIRE(D < (1 << 20));
+  if (rows == 0) return MK_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((rows + 255) / 256));
+#define MK_QKV(T, BB)                                                                 \
+  quantize_kv_rows_kernel<T, BB><<<grid, 256, 0, st>>>((const T*)src, codes, scales, rows, \
+                                                       (int)D, (int)group_size)
+  if (dtype == MK_DT_F16) {
+    if (bits == 8) MK_QKV(f16, 8);
+    else MK_QKV(f16, 4);
+  } else {
+    if (bits == 8) MK_QKV(bf16, 8);
+    else MK_QKV(bf16, 4);
+  }
+#undef MK_QKV
+  MK_CHECK_LAUNCH();
+  return MK_OK;
+}
 
 int mk_block_table_lookup(const int32_t* block_table, const int32_t* positions, int32_t* page_ids,
                           int32_t* offsets, int64_t B, int64_t max_blocks, int64_t page_size,

@@ -59,6 +59,7 @@ SIGNATURES: dict[str, list] = {
     "mk_paged_kv_update": [_P, _P, _P, _P, _P, _P] + [_I64] * 6 + [_I, _P],
     "mk_qkv_rope_paged_update": [_P] * 8 + [_I64] * 8 + [_I, _P],
     "mk_qkv_rope_paged_update_quant": [_P] * 10 + [_I64] * 9 + [_I, _I, _P],
+    "mk_quantize_kv": [_P, _P, _P, _I64, _I64, _I64, _I, _I, _P],
     "mk_paged_attention_workspace_bytes": [_I64] * 6,
     "mk_paged_decode_attention": [_P] * 6 + [_I64] * 7 + [_F, _I, _P, _SZ, _P],
     "mk_paged_quantized_decode_attention": [_P] * 8 + [_I64] * 8 + [_I, _F, _I, _P, _SZ, _P],

@@ -203,15 +203,35 @@ def quantize_kv_pages(K_pages, V_pages, block_table, lengths, config: PagedQuant
         raise ValueError(f"K_pages and V_pages must match, got {tuple(K_pages.shape)} != {tuple(V_pages.shape)}")
     if K_pages.ndim != 4:
         raise ValueError(f"K_pages must be 4-D [NUM_PAGES,PAGE_SIZE,Hkv,D], got {tuple(K_pages.shape)}")
-    kq, ks = _quantize_last_dim(K_pages.to(torch.float32), config.group_size, config.bits)
-    vq, vs = _quantize_last_dim(V_pages.to(torch.float32), config.group_size, config.bits)
-    if config.bits == 4:
-        kq, vq = _pack_last_dim(kq), _pack_last_dim(vq)
+    if K_pages.device.type == "cuda":
+        kq, ks = _hip_quantize_rows(K_pages, config.group_size, config.bits)
+        vq, vs = _hip_quantize_rows(V_pages, config.group_size, config.bits)
+    else:
+        kq, ks = _quantize_last_dim(K_pages.to(torch.float32), config.group_size, config.bits)
+        vq, vs = _quantize_last_dim(V_pages.to(torch.float32), config.group_size, config.bits)
+        if config.bits == 4:
+            kq, vq = _pack_last_dim(kq), _pack_last_dim(vq)
     return PagedQuantizedKVCache(
         k_pages_q=kq, v_pages_q=vq, k_scales=ks, v_scales=vs, block_table=block_table, lengths=lengths,
         bits=config.bits, page_size=config.page_size, group_size=config.group_size,
         original_page_shape=tuple(K_pages.shape),
     )
+
+
+def _hip_quantize_rows(pages: torch.Tensor, group_size: int, bits: int):
+    """mk_quantize_kv over every (page, slot, head) row of a device tensor."""
+    if pages.dtype not in (torch.float16, torch.bfloat16):
+        pages = pages.to(torch.float16)
+    src = pages.contiguous()
+    dev = _lib.require_device(src)
+    *lead, D = src.shape
+    rows = src.numel() // D
+    G = (D + group_size - 1) // group_size
+    codes = torch.empty(tuple(lead) + ((D if bits == 8 else (D + 1) // 2),), dtype=torch.uint8, device=dev)
+    scales = torch.empty(tuple(lead) + (G,), dtype=torch.float16, device=dev)
+    _lib.launch("mk_quantize_kv", dev, _lib.ptr(src), _lib.ptr(codes), _lib.ptr(scales), rows, D, group_size, bits,
+                _lib.dtype_code(src.dtype))
+    return codes, scales
 
 
 def _unpacked_codes(paged_qkv: PagedQuantizedKVCache, which: str, D: int) -> torch.Tensor:

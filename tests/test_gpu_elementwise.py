@@ -1,0 +1,82 @@
+"""HIP rms_norm / residual + rms_norm / SwiGLU / residual add vs the oracle.
+
+Hidden sizes cover both norm kernels: D % 8 == 0 up to 8192 takes the
+register-resident vector kernel (1, 2 or 4 chunks of 8 per thread), other D
+the strided one.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import mk.activation_ops as act_ops
+import mk.fused_ops as fused
+import mk.norm_ops as norm
+from oracle import quant as oq
+from tests._data import assert_close
+
+pytestmark = pytest.mark.gpu
+
+DT = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
+
+
+def _rand(rng, shape, dt, dev, scale=1.0):
+    t = torch.from_numpy((rng.standard_normal(shape) * scale).astype(np.float32)).to(DT[dt])
+    return t.to(dev), t.float().numpy()
+
+
+def _round(a: np.ndarray, dt: str) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(DT[dt]).float().numpy()
+
+
+@pytest.mark.parametrize("D", [8, 1000, 2048, 4096, 4100, 6000, 8192, 12288])
+@pytest.mark.parametrize("xdt,wdt", [("f16", "f16"), ("bf16", "bf16"), ("f16", "f32"), ("f32", "f32"),
+                                     ("bf16", "f16")])
+def test_rms_norm(dev, D, xdt, wdt):
+    rng = np.random.default_rng(D)
+    x, xf = _rand(rng, (3, 1, D), xdt, dev)
+    w, wf = _rand(rng, (D,), wdt, dev, 0.5)
+    got = norm.rms_norm(x, w)
+    assert got.dtype == x.dtype
+    ref = _round(oq.rms_norm(xf, wf), xdt)
+    assert_close(got.float().cpu().numpy(), ref, what=f"rms_norm D={D}")
+
+
+@pytest.mark.parametrize("D", [8, 1000, 4096, 6000, 12288])
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_residual_rms_norm(dev, D, dt):
+    rng = np.random.default_rng(100 + D)
+    x, xf = _rand(rng, (2, 1, D), dt, dev)
+    r, rf = _rand(rng, (2, 1, D), dt, dev)
+    w, wf = _rand(rng, (D,), dt, dev, 0.5)
+    z, y = norm.residual_rms_norm(x, r, w)
+    zref = _round(xf + rf, dt)
+    # z is one rounding of an exact fp32 sum: bit-exact
+    assert np.array_equal(z.float().cpu().numpy(), zref)
+    yref = _round(oq.rms_norm(zref.reshape(2, D), wf), dt).reshape(2, 1, D)
+    assert_close(y.float().cpu().numpy(), yref, what=f"residual_rms_norm D={D}")
+
+
+def test_rms_norm_unaligned_view_uses_strided_kernel(dev):
+    # a view starting one element in is not 16-byte aligned
+    rng = np.random.default_rng(7)
+    base, bf = _rand(rng, (4097,), "f16", dev)
+    w, wf = _rand(rng, (4096,), "f16", dev)
+    x = base[1:].reshape(1, 1, 4096)
+    assert x.data_ptr() % 16 != 0
+    got = norm.rms_norm(x, w)
+    ref = _round(oq.rms_norm(bf[1:].reshape(1, 1, 4096), wf), "f16")
+    assert_close(got.float().cpu().numpy(), ref, what="unaligned rms_norm")
+
+
+@pytest.mark.parametrize("n", [1, 4096, 14336, 100003])
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_swiglu_and_residual_add(dev, n, dt):
+    rng = np.random.default_rng(n)
+    g, gf = _rand(rng, (1, 1, n), dt, dev, 3.0)
+    u, uf = _rand(rng, (1, 1, n), dt, dev)
+    got = act_ops.swiglu(g, u)
+    ref = oq.swiglu(gf, uf, act=dt).astype(np.float32)
+    assert_close(got.float().cpu().numpy(), ref, what="swiglu")
+    s = fused.residual_add(g, u)
+    assert np.array_equal(s.float().cpu().numpy(), _round(gf + uf, dt))
