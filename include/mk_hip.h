@@ -169,10 +169,11 @@ int mk_quantize_kv(const void* src, uint8_t* codes, f16_storage_t* scales, int64
 
 /* ---------------------------------------------------------------- paged decode attention */
 
-/* Workspace (bytes) the split-K attention kernels need for B sequences of at
- * most max_blocks pages, Hq query / Hkv key-value heads of dimension D
- * (0 when no split is needed).  No reference counterpart: the reference's
- * one-thread-per-head kernels do not split the context. */
+/* Scratch (bytes, 16-byte aligned, any content) the split-context attention
+ * kernels need for B sequences of at most max_blocks pages, Hq query / Hkv
+ * key-value heads of dimension D, on the current device.  Calls that may
+ * run concurrently need distinct workspaces.  No reference counterpart: the
+ * reference's one-thread-per-head kernels do not split the context. */
 size_t mk_paged_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
                                           int64_t max_blocks, int64_t page_size);
 

@@ -118,6 +118,11 @@ __device__ __forceinline__ u32x4 ldg128_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
+// 8-byte read that is not expected to be reused (nontemporal)
+__device__ __forceinline__ u32x2 ldg64_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+}
+
 // Hide a constant from the optimizer so it lives in a VGPR: gfx9 VOP3
 // instructions accept at most one scalar/literal operand, and
 // v_and_or_b32(x, mask, magic) needs the magic in a vector register.

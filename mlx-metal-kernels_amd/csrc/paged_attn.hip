@@ -29,7 +29,24 @@
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kTilesPerBlock = 2;  // 32 positions per softmax update
+constexpr int kBlockPos = 32;         // positions per softmax block (two MFMA tiles)
+constexpr int kMaxSplitPages = 512;   // page ids one split may touch (LDS)
+
+// Shortest split (in 32-position blocks): below it a wave's fixed start-up
+// cost outweighs the extra parallelism.
+#ifndef MK_ATTN_MIN_SPLIT_BLOCKS
+#define MK_ATTN_MIN_SPLIT_BLOCKS 8
+#endif
+// Rounds of resident waves the split plan aims for at least (measured: one
+// round is best -- later rounds pay their start-up loads at loaded latency).
+#ifndef MK_ATTN_ROUNDS
+#define MK_ATTN_ROUNDS 1
+#endif
+// MK_ATTN_NT 1 reads K/V pages with nontemporal loads (measured: no gain on
+// balance -- slightly faster for fp16 pages, slower for q8 -- so off).
+#ifndef MK_ATTN_NT
+#define MK_ATTN_NT 0
+#endif
 
 struct PagedArgs {
   const void* q;       // [B, Hq, D]
@@ -40,11 +57,16 @@ struct PagedArgs {
   const int32_t* bt;   // [B, MB]
   const int32_t* lengths;
   void* out;           // [B, Hq, D]
-  float* ws;           // partials
+  float* ws;           // split partials O: [max_pairs][Hq][D] fp32
+  float* ws_ml;        // split partials (m, l): [max_pairs][Hq][2] fp32
   int B, Hq, Hkv, G, HB;
-  int NP, P, MB;
+  int NP, P, MB, lgP;  // fast path: P = 1 << lgP
   int gs, ngroups;     // quantization group size and groups per head
-  int split_tok, s_max;
+  int lg_gs;           // fast path: gs = 1 << lg_gs
+  // fast-path split plan (see plan_pairs): (sequence, split) pairs per round,
+  // the longest split allowed, and the pair count the workspace can hold
+  int T_pairs, cap_tok, max_pairs;
+  int units;           // (kv head, block of 16 query heads) waves per pair
   float scale_log2;
 };
 
@@ -116,311 +138,719 @@ __device__ __forceinline__ u32x4 deq4x8(uint32_t u, f16x2 s2) {
   return r;
 }
 
-// permutation of 8 consecutive d's produced by the dequant helpers, and the
-// matching regroup of q (natural order) into that order
+// --------------------------------------------------------------- fast path
+// One wave per ((sequence, split) pair, kv head [, block of 16 query heads]);
+// the split plan is below.  Lane l is (r16 = l % 16, kb = l / 16).
+//
+//   QK^T : v_mfma_f32_16x16x32, A = K tile (16 positions x 32 d; lane = row
+//          r16, d run kb), B = q^T (32 d x 16 query heads; the GQA group fills
+//          the columns, so one K read serves every head of the group).
+//          Result: lane holds S[position 4kb+i][head r16].
+//   P.V  : v_mfma_f32_16x16x32, A = P (16 heads x 32 positions) -- the two
+//          QK tiles' accumulators as they lie (k = 8kb+i <-> position 4kb+i,
+//          k = 8kb+4+i <-> position 16+4kb+i), B = V (32 positions x 16 d
+//          columns) with the same k <-> position map, one MFMA per d slot.
+//
+// The context of a split streams in blocks of 32 positions, double-buffered
+// in registers: the loads of block i+1 are issued before block i is
+// consumed.  Loads are branch-free -- positions past the split's end or on
+// an unmapped page read a clamped in-bounds row and are masked out of the
+// softmax (their V is zeroed) -- so the compiler's wait counts stay exact.
+// Page ids of the split are read once (see SplitCtx).  Splits that do not
+// finish their sequence write (m, l, O) partials that paged_attn_merge_kernel
+// combines.
+
+__device__ __forceinline__ u32x4 kv_ld128(const void* p) {
+  if constexpr (MK_ATTN_NT) return ldg128_stream(p);
+  else return ldg128(p);
+}
+__device__ __forceinline__ u32x2 kv_ld64(const void* p) {
+  if constexpr (MK_ATTN_NT) return ldg64_stream(p);
+  else return ldg64(p);
+}
+
+template <int KVF, int D>
+struct Fmt {
+  static constexpr int KSTEPS = D / 32;  // QK MFMAs per 16-position tile
+  static constexpr int DPL = D / 16;     // d's per V lane = PV MFMAs per block
+  // 8-d K chunks one lane loads per instruction (16 B for every format but
+  // q4 at D = 64, 8 B)
+  static constexpr int KRUN_RAW = KVF == 0 ? 1 : (KVF == 8 ? 2 : 4);
+  static constexpr int KRUN = KRUN_RAW < KSTEPS ? KRUN_RAW : KSTEPS;
+  static constexpr int NRUN = KSTEPS / KRUN;
+  static constexpr int BITS = KVF == 0 ? 16 : KVF;  // stored bits per element
+  static constexpr int KBYTES_RUN = KRUN * 8 * BITS / 8;
+  static constexpr int VBYTES = DPL * BITS / 8;
+  static constexpr int ROW_BYTES = D * BITS / 8;
+  // first d of step j for lane column kb
+  static __device__ __forceinline__ int dbase(int j, int kb) {
+    return (j / KRUN) * (32 * KRUN) + kb * (8 * KRUN) + (j % KRUN) * 8;
+  }
+  // d (within a lane's V chunk) of the half in slot j after dequant
+  static __device__ __forceinline__ constexpr int vslot(int j) {
+    if constexpr (KVF == 0) {
+      return j;
+    } else if constexpr (DPL == 4) {
+      constexpr int p[4] = {0, 2, 1, 3};
+      return p[j];
+    } else if constexpr (KVF == 8) {
+      constexpr int p[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+      return p[j];
+    } else {
+      constexpr int p[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+      return p[j];
+    }
+  }
+};
+
+// q regrouped into the order the K dequant produces (natural for fp16/bf16)
 template <int KVF>
 __device__ __forceinline__ u32x4 qperm(u32x4 X) {
-  if constexpr (KVF == 8) {
-    u32x4 r;
-    r[0] = (X[0] & 0xFFFFu) | (X[1] << 16);
-    r[1] = (X[0] >> 16) | (X[1] & 0xFFFF0000u);
-    r[2] = (X[2] & 0xFFFFu) | (X[3] << 16);
-    r[3] = (X[2] >> 16) | (X[3] & 0xFFFF0000u);
-    return r;
-  } else if constexpr (KVF == 4) {
-    u32x4 r;
-    r[0] = (X[0] & 0xFFFFu) | (X[2] << 16);
-    r[1] = (X[0] >> 16) | (X[2] & 0xFFFF0000u);
-    r[2] = (X[1] & 0xFFFFu) | (X[3] << 16);
-    r[3] = (X[1] >> 16) | (X[3] & 0xFFFF0000u);
-    return r;
+  if constexpr (KVF == 8) {  // [0,2,1,3,4,6,5,7]
+    return (u32x4){pack_lo16(X[0], X[1]), pack_hi16(X[0], X[1]), pack_lo16(X[2], X[3]),
+                   pack_hi16(X[2], X[3])};
+  } else if constexpr (KVF == 4) {  // [0,4,1,5,2,6,3,7]
+    return (u32x4){pack_lo16(X[0], X[2]), pack_hi16(X[0], X[2]), pack_lo16(X[1], X[3]),
+                   pack_hi16(X[1], X[3])};
   } else {
     return X;
   }
 }
-// slot (0..7) of the permuted vector -> d offset within the 8
-template <int KVF>
-__device__ __forceinline__ int dslot(int j) {
-  if constexpr (KVF == 8) {
-    constexpr int p[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-    return p[j];
-  } else if constexpr (KVF == 4) {
-    constexpr int p[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-    return p[j];
-  } else {
-    return j;
+
+// 4 q8 codes (one word) -> 4 fp16, order [0,2,1,3]; 4 q4 codes (low 16 bits) likewise
+__device__ __forceinline__ u32x2 deq8x4(uint32_t u, f16x2 s2) {
+  return (u32x2){q8_pair(u, 0, s2), q8_pair(u, 8, s2)};
+}
+__device__ __forceinline__ u32x2 deq4x4(uint32_t u, f16x2 s2) {
+  const uint32_t t = (u & 0xFFu) | ((u & 0xFF00u) << 8);  // n0 n1 @ bits 0..7, n2 n3 @ 16..23
+  return (u32x2){q4_pair(t, 0, s2), q4_pair(t, 4, s2)};
+}
+
+__device__ __forceinline__ f16x2 splat_h(uint32_t s) {
+  return bitcast<f16x2>(s | (s << 16));
+}
+
+template <int KVF, int D, bool SB>
+struct KVBlock {
+  using F = Fmt<KVF, D>;
+  static constexpr int NKS = KVF == 0 ? 0 : (SB ? F::NRUN : F::KSTEPS);  // K scales per tile
+  u32x4 k[2][F::NRUN];
+  uint32_t ks[2][NKS > 0 ? NKS : 1];  // fp16 scale bits (32-bit slots keep the block in registers)
+  u32x4 v[8];
+  uint32_t vs[8];
+  uint32_t mask;  // bit p: position p of the block is valid (wave-uniform)
+};
+
+// ------------------------------------------------------------ split plan
+// The work is cut into N (sequence, split) pairs, N a whole number r of
+// rounds of T_pairs (one resident workgroup slot per pair), so that the
+// pairs fill the machine evenly whatever the lengths.  Sequence b gets
+//   n_b = 1 + floor((N-B) cum_b / total) - floor((N-B) cum_{b-1} / total)
+// pairs (cum = inclusive prefix of the lengths): at least one, the rest in
+// proportion to its length, sum exactly N.  Its splits are
+// st_b = ceil(len_b / n_b) rounded up to whole 32-position blocks, so every
+// pair holds about total / (N - B) positions.  r is the smallest count of
+// rounds whose split length stays within cap_tok; N is lowered when the
+// splits would fall below the minimum split length.  Pairs are enumerated
+// sequence-major: consecutive pairs -- which the dispatcher sends to
+// different XCDs -- are different splits.  Every workgroup derives the same
+// plan from the lengths on the device.
+__device__ __forceinline__ int clamp_len(int len, int max_s) {
+  return len < 0 ? 0 : (len > max_s ? max_s : len);
+}
+
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ int64_t wave_incl_scan_i64(int64_t v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+struct PairPlan {
+  int b;       // sequence (-1: past the last pair)
+  int s;       // split of b (>= nsplit: an idle pair)
+  int st;      // positions per split of b
+  int nsplit;  // splits of b actually used
+  int first;   // first pair of b
+  int len;     // positions of b
+};
+
+__device__ __forceinline__ int64_t pairs_before(int64_t extra, int64_t cum, int64_t total) {
+  return total > 0 ? (extra * cum) / total : 0;
+}
+
+// by_seq false: the plan of pair `key`; true: the plan of sequence `key`
+// (its first pair, split length and split count; s = 0).
+__device__ PairPlan plan_pairs(const PagedArgs& a, int key, bool by_seq, int lane) {
+  const int max_s = a.MB << a.lgP;
+  const int64_t B = a.B, T = a.T_pairs;
+  // total length
+  int64_t total = 0;
+  for (int c = 0; c < a.B; c += 64) {
+    const int b = c + lane;
+    total += b < a.B ? clamp_len(a.lengths[b], max_s) : 0;
+  }
+  total = wave_sum_i64(total);
+  // pair count N
+  const int64_t cap_blk = a.cap_tok / kBlockPos;
+  int64_t r = B / T + 1;
+  if (r < MK_ATTN_ROUNDS) r = MK_ATTN_ROUNDS;
+  while ((total + (r * T - B) * kBlockPos - 1) / ((r * T - B) * kBlockPos) > cap_blk) ++r;
+  int64_t N = r * T;
+  const int64_t min_st = (int64_t)(MK_ATTN_MIN_SPLIT_BLOCKS < cap_blk ? MK_ATTN_MIN_SPLIT_BLOCKS : cap_blk) *
+                         kBlockPos;
+  if ((N - B) * min_st > total) N = B + (total + min_st - 1) / min_st;
+  if (N <= B) N = B + 1;
+  const int64_t extra = N - B;
+  // locate the pair: P_b (pairs up to and including b) = b + 1 + floor(extra cum_b / total)
+  PairPlan pl;
+  pl.b = -1;
+  int64_t carry = 0;
+  for (int c = 0; c < a.B; c += 64) {
+    const int b = c + lane;
+    const int len = b < a.B ? clamp_len(a.lengths[b], max_s) : 0;
+    const int64_t cum = wave_incl_scan_i64(len, lane) + carry;
+    const int64_t P_incl = (int64_t)b + 1 + pairs_before(extra, cum, total);
+    const int64_t P_excl = (int64_t)b + pairs_before(extra, cum - len, total);
+    const uint64_t before = __ballot(b < a.B && P_incl <= key);
+    const int k = by_seq ? key - c : __popcll(before);
+    if (k >= 0 && k < 64 && c + k < a.B) {
+      pl.b = c + k;
+      pl.first = (int)__shfl(P_excl, k, 64);
+      pl.len = __shfl(len, k, 64);
+      const int n_b = (int)(__shfl(P_incl, k, 64) - pl.first);
+      pl.s = by_seq ? 0 : key - pl.first;
+      int st = (pl.len + n_b - 1) / n_b;
+      st = (st + kBlockPos - 1) / kBlockPos * kBlockPos;
+      pl.st = st < kBlockPos ? kBlockPos : st;
+      pl.nsplit = pl.len > 0 ? (pl.len + pl.st - 1) / pl.st : 1;
+      return pl;
+    }
+    carry = __shfl(cum, 63, 64);
+  }
+  return pl;
+}
+
+// Merge the split partials of query heads [h0, h0 + hcount) of sequence b
+// (LSE merge, ops/attention_ops.py:534-550): one wave, lanes over d.
+template <typename AT, int D>
+__device__ void merge_heads(const PagedArgs& a, int b, int h0, int hcount, int first, int nsplit,
+                            int lane) {
+  constexpr int DPT = D / 64;  // d's per lane
+  const size_t sstride = (size_t)a.Hq;  // slots between consecutive splits of one head
+  for (int hh = 0; hh < hcount; ++hh) {
+    const int h = h0 + hh;
+    const float* ml = a.ws_ml + ((size_t)first * a.Hq + h) * 2;
+    const float* po = a.ws + ((size_t)first * a.Hq + h) * D + lane * DPT;
+    float M = -INFINITY;
+    for (int s0 = 0; s0 < nsplit; s0 += 64) {
+      const int s = s0 + lane;
+      M = fmaxf(M, s < nsplit ? ml[(size_t)s * sstride * 2] : -INFINITY);
+    }
+    M = wave_max(M);
+    const float Mu = M == -INFINITY ? 0.0f : M;
+    float acc[DPT];
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) acc[e] = 0.0f;
+    float L = 0.0f;
+    for (int s0 = 0; s0 < nsplit; s0 += 64) {
+      const int s = s0 + lane;
+      const f32x2 v = s < nsplit ? *reinterpret_cast<const f32x2*>(ml + (size_t)s * sstride * 2)
+                                 : (f32x2){-INFINITY, 0.0f};
+      const float w = __builtin_amdgcn_exp2f(v[0] - Mu);
+      L += v[1] * w;
+      const int n = min(64, nsplit - s0);
+      int t = 0;
+      for (; t + 4 <= n; t += 4) {
+        float x[4][DPT], ws[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          ws[k] = __shfl(w, t + k, 64);
+          const float* p = po + (size_t)(s0 + t + k) * sstride * D;
+          if constexpr (DPT == 2) {
+            const f32x2 y = *reinterpret_cast<const f32x2*>(p);
+            x[k][0] = y[0];
+            x[k][1] = y[1];
+          } else {
+            x[k][0] = p[0];
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int e = 0; e < DPT; ++e) acc[e] += ws[k] * x[k][e];
+      }
+      for (; t < n; ++t) {
+        const float wt = __shfl(w, t, 64);
+        const float* p = po + (size_t)(s0 + t) * sstride * D;
+#pragma unroll
+        for (int e = 0; e < DPT; ++e) acc[e] += wt * p[e];
+      }
+    }
+    L = wave_sum(L);
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    AT* op = reinterpret_cast<AT*>(a.out) + ((size_t)b * a.Hq + h) * D + lane * DPT;
+    if constexpr (DPT == 2) {
+      *reinterpret_cast<uint32_t*>(op) = pack_act2<AT>(acc[0] * inv, acc[1] * inv);
+    } else {
+      op[0] = from_f32<AT>(acc[0] * inv);
+    }
   }
 }
 
-__device__ __forceinline__ f16x2 scale2(const uint16_t* sp) {
-  const f16 s = bitcast<f16>(*sp);
-  return (f16x2){s, s};
-}
-
-// Load 8 consecutive d's [d0, d0+8) of one K or V row as 8 act-type values
-// (permuted order for quantized formats).  row_elem = (page*P+off)*Hkv+hkv.
-template <typename AT, int D, int KVF>
-__device__ __forceinline__ u32x4 load8(const void* base, const uint16_t* sbase, size_t row_elem,
-                                       int d0, int gs, int ngroups) {
-  if constexpr (KVF == 0) {
-    return ldg128(reinterpret_cast<const AT*>(base) + row_elem * D + d0);
-  } else if constexpr (KVF == 8) {
-    const u32x2 c = ldg64(reinterpret_cast<const uint8_t*>(base) + row_elem * D + d0);
-    const f16x2 s2 = scale2(sbase + row_elem * ngroups + d0 / gs);
-    return deq8x8(c[0], c[1], s2);
-  } else {
-    const uint32_t c =
-        *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(base) +
-                                           row_elem * (D / 2) + d0 / 2);
-    const f16x2 s2 = scale2(sbase + row_elem * ngroups + d0 / gs);
-    return deq4x8(c, s2);
-  }
-}
-
-// --------------------------------------------------------------- main kernel
-template <typename AT, int D, int KVF>
-__global__ __launch_bounds__(64) void paged_attn_kernel(const PagedArgs a) {
-  constexpr int DQ = D / 4;         // d's per K-load lane
-  constexpr int KSTEPS = D / 32;    // QK MFMAs per tile
-  constexpr int DPL = D / 16;       // d's per output column lane (PV MFMAs per tile)
-  static_assert(DPL == 8 || DPL == 4, "D must be 64 or 128");
-
+// One wave per (sequence, query head): merges the head's split partials
+// (sequences finished in one split were written by the attention kernel).
+template <typename AT, int D>
+__global__ __launch_bounds__(64) void paged_attn_merge_kernel(const PagedArgs a) {
   const int lane = threadIdx.x;
+  const int b = (int)blockIdx.x / a.Hq;
+  const int h = (int)blockIdx.x - b * a.Hq;
+  const PairPlan pl = plan_pairs(a, b, true, lane);
+  if (pl.nsplit <= 1) return;
+  merge_heads<AT, D>(a, b, h, 1, pl.first, pl.nsplit, lane);
+}
+
+// Where one split's positions live.  Two addressing modes:
+//  * PT (page size a multiple of 16): a 16-position tile never crosses a
+//    page, so each tile needs one page id -- read from a register that holds
+//    the split's page ids (lane i: page i, at most 64) -- and the tile's row
+//    base is wave-uniform; lanes add fixed offsets.
+//  * otherwise: every position looks its page up in an LDS copy of the
+//    split's block-table row.
+struct SplitCtx {
+  const int* spage;  // !PT: LDS page ids of the split (invalid as -1)
+  int my_page;       // PT: page id of logical block blk0 + lane (invalid as -1)
+  int blk0;          // first logical block of the split
+  int t_begin, t_end, lgP, Pm, Hkv, hkv;
+  // !PT: row index (page, slot, kv head) of position t, clamped into the
+  // split; *ok says whether t is a real, mapped position
+  __device__ __forceinline__ uint32_t row(int t, bool* ok) const {
+    const bool in = t < t_end;
+    const int tc = in ? t : t_end - 1;
+    const int pg = spage[(tc >> lgP) - blk0];
+    *ok = in && pg >= 0;
+    const uint32_t p = pg < 0 ? 0u : (uint32_t)pg;
+    return (((p << lgP) + (uint32_t)(tc & Pm)) * (uint32_t)Hkv) + (uint32_t)hkv;
+  }
+  // PT: row index of the first position of the 16-position tile at tu
+  // (clamped to the split's last tile) and the tile's validity bits
+  __device__ __forceinline__ uint32_t tile_row(int tu, uint32_t* bits) const {
+    const int last = (t_end - 1) & ~15;
+    const int tc = tu < last ? tu : last;
+    const int pg = __builtin_amdgcn_readlane(my_page, (tc >> lgP) - blk0);
+    int n = t_end - tu;
+    n = n < 0 ? 0 : (n > 16 ? 16 : n);
+    *bits = pg < 0 ? 0u : (n == 16 ? 0xFFFFu : ((1u << n) - 1u));
+    const uint32_t p = pg < 0 ? 0u : (uint32_t)pg;
+    return (((p << lgP) + (uint32_t)(tc & Pm)) * (uint32_t)Hkv) + (uint32_t)hkv;
+  }
+};
+
+// Lane-constant byte offsets of the PT addressing mode.
+template <int KVF, int D, bool SB>
+struct LaneOffsets {
+  using F = Fmt<KVF, D>;
+  static constexpr int NKS = KVF == 0 ? 0 : (SB ? F::NRUN : F::KSTEPS);
+  uint32_t k[F::NRUN];            // K codes of run r of row r16
+  uint32_t v[4];                  // V chunk of row 4kb + i
+  uint32_t ks[NKS > 0 ? NKS : 1];  // K scale (elements) of the lane's chunks
+  uint32_t vs[4];                 // V scale (elements)
+};
+
+template <typename AT, int D, int KVF, bool SB, bool PT>
+__device__ __forceinline__ void load_block(KVBlock<KVF, D, SB>& blk, const PagedArgs& a,
+                                           const SplitCtx& c, const LaneOffsets<KVF, D, SB>& lo,
+                                           int tb, int r16, int kb) {
+  using F = Fmt<KVF, D>;
+  constexpr int NKS = KVBlock<KVF, D, SB>::NKS;
+  const uint8_t* Kb = reinterpret_cast<const uint8_t*>(a.K);
+  const uint8_t* Vb = reinterpret_cast<const uint8_t*>(a.V);
+  if constexpr (PT) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      uint32_t bits;
+      const uint32_t row0 = c.tile_row(tb + 16 * u, &bits);
+      m |= bits << (16 * u);
+      const uint8_t* kt = Kb + (uint64_t)row0 * F::ROW_BYTES;
+      const uint8_t* vt = Vb + (uint64_t)row0 * F::ROW_BYTES;
+#pragma unroll
+      for (int r = 0; r < F::NRUN; ++r) {
+        if constexpr (F::KBYTES_RUN == 16) {
+          blk.k[u][r] = kv_ld128(kt + lo.k[r]);
+        } else {
+          const u32x2 x = kv_ld64(kt + lo.k[r]);
+          blk.k[u][r] = (u32x4){x[0], x[1], 0u, 0u};
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint8_t* vr = vt + lo.v[i];
+        u32x4 x;
+        if constexpr (F::VBYTES == 16) {
+          x = kv_ld128(vr);
+        } else if constexpr (F::VBYTES == 8) {
+          const u32x2 y = kv_ld64(vr);
+          x = (u32x4){y[0], y[1], 0u, 0u};
+        } else if constexpr (F::VBYTES == 4) {
+          x = (u32x4){*reinterpret_cast<const uint32_t*>(vr), 0u, 0u, 0u};
+        } else {
+          x = (u32x4){(uint32_t)*reinterpret_cast<const uint16_t*>(vr), 0u, 0u, 0u};
+        }
+        blk.v[4 * u + i] = x;
+      }
+      if constexpr (KVF != 0) {
+        const uint16_t* kst = a.Ks + (uint64_t)row0 * a.ngroups;
+        const uint16_t* vst = a.Vs + (uint64_t)row0 * a.ngroups;
+#pragma unroll
+        for (int e = 0; e < NKS; ++e) blk.ks[u][e] = kst[lo.ks[e]];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) blk.vs[4 * u + i] = vst[lo.vs[i]];
+      }
+    }
+    blk.mask = m;
+  } else {
+    uint32_t m = 0;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      bool ok;
+      const uint32_t row = c.row(tb + 16 * u + r16, &ok);
+      const uint8_t* kr = Kb + (uint64_t)row * F::ROW_BYTES;
+#pragma unroll
+      for (int r = 0; r < F::NRUN; ++r) {
+        const int off = F::dbase(r * F::KRUN, kb) * F::BITS / 8;
+        if constexpr (F::KBYTES_RUN == 16) {
+          blk.k[u][r] = kv_ld128(kr + off);
+        } else {
+          const u32x2 x = kv_ld64(kr + off);
+          blk.k[u][r] = (u32x4){x[0], x[1], 0u, 0u};
+        }
+      }
+      if constexpr (KVF != 0) {
+        const uint16_t* sr = a.Ks + (uint64_t)row * a.ngroups;
+#pragma unroll
+        for (int e = 0; e < NKS; ++e) {
+          const int j = SB ? e * F::KRUN : e;
+          blk.ks[u][e] = sr[F::dbase(j, kb) >> a.lg_gs];
+        }
+      }
+      const uint64_t bal = __ballot(ok);
+      m |= ((uint32_t)bal & 0xFFFFu) << (16 * u);
+    }
+    blk.mask = m;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      bool ok;
+      const int pos = (p < 4 ? 4 * kb + p : 16 + 4 * kb + (p - 4));
+      const uint32_t row = c.row(tb + pos, &ok);
+      const uint8_t* vr = Vb + (uint64_t)row * F::ROW_BYTES + r16 * F::VBYTES;
+      if constexpr (F::VBYTES == 16) {
+        blk.v[p] = kv_ld128(vr);
+      } else if constexpr (F::VBYTES == 8) {
+        const u32x2 x = kv_ld64(vr);
+        blk.v[p] = (u32x4){x[0], x[1], 0u, 0u};
+      } else if constexpr (F::VBYTES == 4) {
+        blk.v[p] = (u32x4){*reinterpret_cast<const uint32_t*>(vr), 0u, 0u, 0u};
+      } else {
+        blk.v[p] = (u32x4){(uint32_t)*reinterpret_cast<const uint16_t*>(vr), 0u, 0u, 0u};
+      }
+      if constexpr (KVF != 0)
+        blk.vs[p] = a.Vs[(uint64_t)row * a.ngroups + ((r16 * F::DPL) >> a.lg_gs)];
+    }
+  }
+}
+
+// 8 act-type values of K step j (order as qperm<KVF>)
+template <typename AT, int D, int KVF, bool SB>
+__device__ __forceinline__ u32x4 k_operand(const KVBlock<KVF, D, SB>& blk, int u, int j) {
+  using F = Fmt<KVF, D>;
+  const int r = j / F::KRUN, e = j % F::KRUN;
+  if constexpr (KVF == 0) {
+    return blk.k[u][r];
+  } else {
+    const f16x2 s2 = splat_h(blk.ks[u][SB ? r : j]);
+    if constexpr (KVF == 8) return deq8x8(blk.k[u][r][2 * e], blk.k[u][r][2 * e + 1], s2);
+    else return deq4x8(blk.k[u][r][e], s2);
+  }
+}
+
+// V chunk of position p as DPL act-type values in slot order (Fmt::vslot)
+template <int D, int KVF, bool SB>
+__device__ __forceinline__ u32x4 v_chunk(const KVBlock<KVF, D, SB>& blk, int p) {
+  if constexpr (KVF == 0) {
+    return blk.v[p];
+  } else {
+    const f16x2 s2 = splat_h(blk.vs[p]);
+    if constexpr (D == 128) {
+      if constexpr (KVF == 8) return deq8x8(blk.v[p][0], blk.v[p][1], s2);
+      else return deq4x8(blk.v[p][0], s2);
+    } else {
+      const u32x2 x = KVF == 8 ? deq8x4(blk.v[p][0], s2) : deq4x4(blk.v[p][0], s2);
+      return (u32x4){x[0], x[1], 0u, 0u};
+    }
+  }
+}
+
+// Softmax scores are kept in base 2.  The running max of a head is only
+// raised when a block's max exceeds it by more than kLazyMax (so p <= 2^8,
+// exact in fp16/bf16 exponent range); the O rescale runs only then.
+constexpr float kLazyMax = 8.0f;
+
+template <typename AT, int D, int KVF, bool SB, bool PT>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void paged_attn_kernel(
+    const PagedArgs a) {
+  using F = Fmt<KVF, D>;
+  using Blk = KVBlock<KVF, D, SB>;
+  constexpr int KSTEPS = F::KSTEPS;
+  constexpr int DPL = F::DPL;
+
+  const int lane = threadIdx.x & 63;
   const int r16 = lane & 15;
   const int kb = lane >> 4;
-  const int s = blockIdx.x;
-  const int hkv = blockIdx.y / a.HB;
-  const int hb = blockIdx.y - hkv * a.HB;
-  const int b = blockIdx.z;
-
-  int len = a.lengths[b];
-  const int max_s = a.MB * a.P;
-  len = len < 0 ? 0 : (len > max_s ? max_s : len);
-  const int nsplit = len == 0 ? 1 : (len + a.split_tok - 1) / a.split_tok;
-  if (s >= nsplit) return;
-  const int t_begin = s * a.split_tok;
-  const int t_end = min(len, t_begin + a.split_tok);
-
+  // workgroup -> (pair, unit group); wave -> (kv head, block of 16 query heads)
+  // one wave per (pair, unit): consecutive waves are the units of one pair
+  const int pair = (int)blockIdx.x / a.units;
+  const int unit = (int)blockIdx.x - pair * a.units;
+  const int hkv = unit / a.HB;
+  const int hb = unit - hkv * a.HB;
+  const PairPlan pl = plan_pairs(a, pair, false, lane);
+  // past the last pair, or a pair the rounding of its sequence's split
+  // length left empty
+  if (pl.b < 0 || pl.s >= pl.nsplit) return;
+  const int b = pl.b, s = pl.s, nsplit = pl.nsplit;
+  const int t_begin = s * pl.st;
+  const int t_end = min(pl.len, t_begin + pl.st);
   const int h0 = hkv * a.G + hb * 16;
   const int hcount = min(16, a.G - hb * 16);
 
-  // q^T operand: lane (h = r16, kb) holds q[h][kb*DQ + 8j .. +8] for step j
-  u32x4 qv[KSTEPS];
-  {
-    const bool hv = r16 < hcount;
-    const AT* qp = reinterpret_cast<const AT*>(a.q) + ((size_t)b * a.Hq + h0 + (hv ? r16 : 0)) * D +
-                   kb * DQ;
-#pragma unroll
-    for (int j = 0; j < KSTEPS; ++j) {
-      qv[j] = hv ? qperm<KVF>(ldg128(qp + 8 * j)) : (u32x4){0u, 0u, 0u, 0u};
+  __shared__ int spage[PT ? 1 : kMaxSplitPages];
+  SplitCtx c;
+  c.spage = spage;
+  c.my_page = -1;
+  c.t_begin = t_begin;
+  c.t_end = t_end;
+  c.lgP = a.lgP;
+  c.Pm = (1 << a.lgP) - 1;
+  c.Hkv = a.Hkv;
+  c.hkv = hkv;
+  c.blk0 = t_begin >> a.lgP;
+  const int npg = t_end > t_begin ? ((t_end - 1) >> a.lgP) - c.blk0 + 1 : 0;
+  const int32_t* btrow = a.bt + (size_t)b * a.MB + c.blk0;
+  if constexpr (PT) {
+    // the host keeps a split within 64 pages in this mode
+    if (lane < npg) {
+      const int p = btrow[lane];
+      c.my_page = (p >= 0 && p < a.NP) ? p : -1;
+    }
+  } else {
+    for (int i = threadIdx.x; i < npg; i += blockDim.x) {
+      const int p = btrow[i];
+      spage[i] = (p >= 0 && p < a.NP) ? p : -1;
     }
   }
 
-  float m_run = -INFINITY;  // per head h = r16 (replicated over kb)
+  LaneOffsets<KVF, D, SB> lo;
+  if constexpr (PT) {
+    const uint32_t rs = (uint32_t)a.Hkv * F::ROW_BYTES;  // bytes between positions of a page
+#pragma unroll
+    for (int r = 0; r < F::NRUN; ++r)
+      lo.k[r] = (uint32_t)r16 * rs + (uint32_t)(F::dbase(r * F::KRUN, kb) * F::BITS / 8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lo.v[i] = (uint32_t)(4 * kb + i) * rs + (uint32_t)(r16 * F::VBYTES);
+    if constexpr (KVF != 0) {
+      const uint32_t ss = (uint32_t)a.Hkv * a.ngroups;  // scale elements between positions
+#pragma unroll
+      for (int e = 0; e < Blk::NKS; ++e) {
+        const int j = SB ? e * F::KRUN : e;
+        lo.ks[e] = (uint32_t)r16 * ss + (uint32_t)(F::dbase(j, kb) >> a.lg_gs);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lo.vs[i] = (uint32_t)(4 * kb + i) * ss + (uint32_t)((r16 * DPL) >> a.lg_gs);
+    }
+  }
+
+  // q^T operand: lane (head r16, kb) holds q[h0 + r16][dbase(j, kb) .. +8] for step j
+  u32x4 qv[KSTEPS];
+  {
+    const bool hv = r16 < hcount;
+    const AT* qp = reinterpret_cast<const AT*>(a.q) + ((size_t)b * a.Hq + h0 + (hv ? r16 : 0)) * D;
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) {
+      const u32x4 x = ldg128(qp + F::dbase(j, kb));
+      qv[j] = hv ? qperm<KVF>(x) : (u32x4){0u, 0u, 0u, 0u};
+    }
+  }
+  if constexpr (!PT) __syncthreads();
+
+  float m_run = -INFINITY;  // per head r16 (replicated over kb)
   float l_run = 0.0f;
   f32x4 o[DPL];
 #pragma unroll
   for (int j = 0; j < DPL; ++j) o[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  const int32_t* btrow = a.bt + (size_t)b * a.MB;
-  const int P = a.P;
-
-  for (int tb = t_begin; tb < t_end; tb += 16 * kTilesPerBlock) {
-    f32x4 sc[kTilesPerBlock];
-    int pg[kTilesPerBlock];
-    uint64_t vmask[kTilesPerBlock];
-    u32x4 vv[kTilesPerBlock][4];
-
+  auto consume = [&](const Blk& blk) {
+    // ---- S^T = K q^T for the two 16-position tiles
+    f32x4 sc[2];
 #pragma unroll
-    for (int u = 0; u < kTilesPerBlock; ++u) {
-      const int tt0 = tb + 16 * u;
-      // K-load lane: position tt0 + r16, d in [kb*DQ, kb*DQ + DQ)
-      const int t = tt0 + r16;
-      int page = -1;
-      if (t < t_end) page = btrow[t / P];
-      const bool valid = page >= 0 && page < a.NP;
-      pg[u] = valid ? page : -1;
-      vmask[u] = __ballot(valid);
-      const size_t row = valid ? ((size_t)page * P + (t % P)) * a.Hkv + hkv : 0;
+    for (int u = 0; u < 2; ++u) {
       f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < KSTEPS; ++j) {
-        const u32x4 kv = valid ? load8<AT, D, KVF>(a.K, a.Ks, row, kb * DQ + 8 * j, a.gs, a.ngroups)
-                               : (u32x4){0u, 0u, 0u, 0u};
-        acc = mfma_k32<AT>(kv, qv[j], acc);
-      }
+      for (int j = 0; j < KSTEPS; ++j) acc = mfma_k32<AT>(k_operand<AT, D, KVF, SB>(blk, u, j), qv[j], acc);
       sc[u] = acc;
-      // V-load lane (column r16, kb): positions tt0 + 4kb + i, d in [r16*DPL, +DPL)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int src = 4 * kb + i;
-        const int vp = __shfl(pg[u], src, 64);
-        const int tv = tt0 + src;
-        if (vp >= 0) {
-          const size_t vrow = ((size_t)vp * P + (tv % P)) * a.Hkv + hkv;
-          if constexpr (DPL == 8) {
-            vv[u][i] = load8<AT, D, KVF>(a.V, a.Vs, vrow, r16 * 8, a.gs, a.ngroups);
-          } else {
-            // 4 d's per lane: natural order for every format
-            if constexpr (KVF == 0) {
-              const u32x2 x = ldg64(reinterpret_cast<const AT*>(a.V) + vrow * D + r16 * 4);
-              vv[u][i] = (u32x4){x[0], x[1], 0u, 0u};
-            } else {
-              const uint16_t* sp = a.Vs + vrow * a.ngroups + (r16 * 4) / a.gs;
-              const float sf = (float)bitcast<f16>(*sp);
-              float w[4];
-              if constexpr (KVF == 8) {
-                const uint32_t c = *reinterpret_cast<const uint32_t*>(
-                    reinterpret_cast<const uint8_t*>(a.V) + vrow * D + r16 * 4);
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                  w[e] = (float)(f16)(((float)((c >> (8 * e)) & 255u) - 128.0f) * sf);
-              } else {
-                const uint16_t c = *reinterpret_cast<const uint16_t*>(
-                    reinterpret_cast<const uint8_t*>(a.V) + vrow * (D / 2) + r16 * 2);
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                  w[e] = (float)(f16)(((float)((c >> (4 * e)) & 15u) - 8.0f) * sf);
-              }
-              vv[u][i] = (u32x4){pack_h2(w[0], w[1]), pack_h2(w[2], w[3]), 0u, 0u};
-            }
-          }
-        } else {
-          vv[u][i] = (u32x4){0u, 0u, 0u, 0u};
-        }
-      }
     }
-
-    // ---- online softmax (base 2) over the block; lane holds S[h=r16][pos 4kb+i]
-    float sv[kTilesPerBlock][4];
-    float bmax = -INFINITY;
+    // ---- scores (base 2); lane holds S[16u + 4kb + i][head r16]
+    float sv[2][4];
 #pragma unroll
-    for (int u = 0; u < kTilesPerBlock; ++u) {
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool ok = (vmask[u] >> (4 * kb + i)) & 1ull;
-        sv[u][i] = ok ? sc[u][i] * a.scale_log2 : -INFINITY;
-        bmax = fmaxf(bmax, sv[u][i]);
-      }
+      for (int i = 0; i < 4; ++i) sv[u][i] = sc[u][i] * a.scale_log2;
+    const bool full = blk.mask == 0xFFFFFFFFu;  // wave-uniform
+    if (!full) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (!((blk.mask >> (16 * u + 4 * kb + i)) & 1u)) sv[u][i] = -INFINITY;
     }
+    float bmax = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
+                       fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
     bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-    const float m_new = fmaxf(m_run, bmax);
-    const float alpha = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - m_new);
+    // lazy max: raise m only when the block exceeds it by more than kLazyMax
+    const bool raise = bmax > m_run + kLazyMax;
+    const float m_new = raise ? bmax : m_run;
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // an all-masked head keeps p = 0
     float psum = 0.0f;
-    u32x2 pa[kTilesPerBlock];
+    float p[2][4];
 #pragma unroll
-    for (int u = 0; u < kTilesPerBlock; ++u) {
-      float p[4];
+    for (int u = 0; u < 2; ++u) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        p[i] = (sv[u][i] == -INFINITY) ? 0.0f : exp2f(sv[u][i] - m_new);
-        psum += p[i];
+        p[u][i] = __builtin_amdgcn_exp2f(sv[u][i] - m_use);
+        psum += p[u][i];
       }
-      pa[u] = (u32x2){pack_act2<AT>(p[0], p[1]), pack_act2<AT>(p[2], p[3])};
     }
     psum += __shfl_xor(psum, 16, 64);
     psum += __shfl_xor(psum, 32, 64);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-
-    // ---- rescale O: lane holds O[h = 4kb + i][col r16]
-    float al[4];
+    if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform: some head's max moved
+      const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
+      l_run *= alpha;
+      // O lane holds O[head 4kb + i][column r16]
 #pragma unroll
-    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * kb + i, 64);
+      for (int i = 0; i < 4; ++i) {
+        const float al = __shfl(alpha, 4 * kb + i, 64);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) o[j][i] *= al;
+      }
+    }
+    l_run += psum;
+    m_run = m_new;
+    const u32x4 pa = {pack_act2<AT>(p[0][0], p[0][1]), pack_act2<AT>(p[0][2], p[0][3]),
+                      pack_act2<AT>(p[1][0], p[1][1]), pack_act2<AT>(p[1][2], p[1][3])};
+
+    // ---- V operand chunks; masked positions are zeroed so stale or non-finite
+    // cache contents cannot reach the output through p = 0
+    u32x4 vc[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) vc[q] = v_chunk<D, KVF, SB>(blk, q);
+    if (!full) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int pos = q < 4 ? 4 * kb + q : 16 + 4 * kb + (q - 4);
+        if (!((blk.mask >> pos) & 1u)) vc[q] = (u32x4){0u, 0u, 0u, 0u};
+      }
+    }
+    // ---- O += P V, one MFMA per d slot
 #pragma unroll
     for (int j = 0; j < DPL; ++j) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[j][i] *= al[i];
-    }
-
-    // ---- O += P . V
-#pragma unroll
-    for (int u = 0; u < kTilesPerBlock; ++u) {
-#pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        // B operand: V[pos 4kb+i][d slot j] for i = 0..3
-        const int w = j >> 1;
-        const int sh = (j & 1) * 16;
-        const uint32_t v0 = (vv[u][0][w] >> sh) & 0xFFFFu;
-        const uint32_t v1 = (vv[u][1][w] >> sh) & 0xFFFFu;
-        const uint32_t v2 = (vv[u][2][w] >> sh) & 0xFFFFu;
-        const uint32_t v3 = (vv[u][3][w] >> sh) & 0xFFFFu;
-        const u32x2 bop = {v0 | (v1 << 16), v2 | (v3 << 16)};
-        o[j] = mfma_k16<AT>(pa[u], bop, o[j]);
+      const int w = j >> 1;
+      u32x4 bop;
+      if (j & 1) {
+        bop = (u32x4){pack_hi16(vc[0][w], vc[1][w]), pack_hi16(vc[2][w], vc[3][w]),
+                      pack_hi16(vc[4][w], vc[5][w]), pack_hi16(vc[6][w], vc[7][w])};
+      } else {
+        bop = (u32x4){pack_lo16(vc[0][w], vc[1][w]), pack_lo16(vc[2][w], vc[3][w]),
+                      pack_lo16(vc[4][w], vc[5][w]), pack_lo16(vc[6][w], vc[7][w])};
       }
+      o[j] = mfma_k32<AT>(pa, bop, o[j]);
     }
-  }
+  };
 
-  // ---- write: lane holds O[h = 4kb + i][d = r16*DPL + slot j]
-  float lv[4];
+  // Blocks 2k and 2k+1 stream through buffers A and B.  Each buffer has one
+  // load site, so its registers are the same on every trip; B starts empty
+  // (mask 0: consuming it changes nothing) and a block index past the end is
+  // clamped to the last block and masked off.
+  const int nblk = (t_end - t_begin + kBlockPos - 1) / kBlockPos;  // 0 for an empty sequence
+  Blk A, Bq;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) lv[i] = __shfl(l_run, 4 * kb + i, 64);
-  if (nsplit == 1) {
+  for (int u = 0; u < 2; ++u)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * kb + i;
-      if (h >= hcount) continue;
+    for (int r = 0; r < F::NRUN; ++r) Bq.k[u][r] = (u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int q = 0; q < 8; ++q) Bq.v[q] = (u32x4){0u, 0u, 0u, 0u};
+  if constexpr (KVF != 0) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int e = 0; e < Blk::NKS; ++e) Bq.ks[u][e] = 0u;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) Bq.vs[q] = 0u;
+  }
+  Bq.mask = 0u;
+  for (int i = 0; i < nblk; i += 2) {
+    load_block<AT, D, KVF, SB, PT>(A, a, c, lo, t_begin + kBlockPos * i, r16, kb);
+    __builtin_amdgcn_sched_barrier(0);
+    consume(Bq);  // block i-1 (empty on the first trip)
+    const bool has1 = i + 1 < nblk;
+    load_block<AT, D, KVF, SB, PT>(Bq, a, c, lo, t_begin + kBlockPos * (has1 ? i + 1 : i), r16, kb);
+    if (!has1) Bq.mask = 0u;
+    __builtin_amdgcn_sched_barrier(0);
+    consume(A);
+  }
+  consume(Bq);  // the last odd block (or an empty one)
+
+  // ---- write: lane holds O[head 4kb + i][d = r16*DPL + vslot(j)]
+  float lv[4], mv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lv[i] = __shfl(l_run, 4 * kb + i, 64);
+    mv[i] = __shfl(m_run, 4 * kb + i, 64);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int h = 4 * kb + i;
+    if (h >= hcount) continue;
+    const size_t bh = (size_t)b * a.Hq + h0 + h;
+    float nat[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) nat[F::vslot(j)] = o[j][i];
+    if (nsplit == 1) {
       const float inv = lv[i] > 0.0f ? 1.0f / lv[i] : 0.0f;
-      AT* op = reinterpret_cast<AT*>(a.out) + ((size_t)b * a.Hq + h0 + h) * D + r16 * DPL;
+      uint32_t w[DPL / 2];
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        const int d = DPL == 8 ? dslot<KVF>(j) : j;
-        op[d] = from_f32<AT>(o[j][i] * inv);
-      }
-    }
-  } else {
-    float mv[4];
+      for (int e = 0; e < DPL / 2; ++e) w[e] = pack_act2<AT>(nat[2 * e] * inv, nat[2 * e + 1] * inv);
+      AT* op = reinterpret_cast<AT*>(a.out) + bh * D + r16 * DPL;
+      if constexpr (DPL == 8) *reinterpret_cast<u32x4*>(op) = (u32x4){w[0], w[1], w[2], w[3]};
+      else *reinterpret_cast<u32x2*>(op) = (u32x2){w[0], w[1]};
+    } else {
+      const size_t slot = (size_t)(pl.first + s) * a.Hq + (bh - (size_t)b * a.Hq);
+      float* po = a.ws + slot * D + r16 * DPL;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mv[i] = __shfl(m_run, 4 * kb + i, 64);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * kb + i;
-      if (h >= hcount) continue;
-      const size_t slot = ((size_t)b * a.Hq + h0 + h) * a.s_max + s;
-      float* po = a.ws + slot * (D + 2);
-#pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        const int d = DPL == 8 ? dslot<KVF>(j) : j;
-        po[r16 * DPL + d] = o[j][i];
-      }
+      for (int e = 0; e < DPL / 4; ++e)
+        reinterpret_cast<f32x4*>(po)[e] = (f32x4){nat[4 * e], nat[4 * e + 1], nat[4 * e + 2], nat[4 * e + 3]};
       if (r16 == 0) {
-        po[D] = mv[i];
-        po[D + 1] = lv[i];
+        float* pml = a.ws_ml + slot * 2;
+        *reinterpret_cast<f32x2*>(pml) = (f32x2){mv[i], lv[i]};
       }
     }
-  }
-}
-
-// LSE merge of the split partials of one (sequence, head): one wave, lanes over d.
-template <typename AT>
-__global__ __launch_bounds__(64) void paged_attn_merge_kernel(const PagedArgs a, int D) {
-  const int bh = blockIdx.x;
-  const int b = bh / a.Hq;
-  int len = a.lengths[b];
-  const int max_s = a.MB * a.P;
-  len = len < 0 ? 0 : (len > max_s ? max_s : len);
-  const int nsplit = len == 0 ? 1 : (len + a.split_tok - 1) / a.split_tok;
-  if (nsplit <= 1) return;
-  const float* base = a.ws + (size_t)bh * a.s_max * (D + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, base[(size_t)s * (D + 2) + D]);
-  float L = 0.0f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float* p = base + (size_t)s * (D + 2);
-    const float m = p[D];
-    if (m != -INFINITY) L += p[D + 1] * exp2f(m - M);
-  }
-  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  AT* op = reinterpret_cast<AT*>(a.out) + (size_t)bh * D;
-  for (int d = threadIdx.x; d < D; d += 64) {
-    float acc = 0.0f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float* p = base + (size_t)s * (D + 2);
-      const float m = p[D];
-      if (m != -INFINITY) acc += p[d] * exp2f(m - M);
-    }
-    op[d] = from_f32<AT>(acc * inv);
   }
 }
 
@@ -503,64 +933,120 @@ __global__ __launch_bounds__(64) void paged_attn_generic_kernel(const PagedArgs 
 }
 
 // --------------------------------------------------------------- host side
-// Positions per split: aim for ~16 waves per CU over the worst-case context.
-inline int choose_split_tokens(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_ctx) {
-  const int64_t hb = ((Hq / (Hkv > 0 ? Hkv : 1)) + 15) / 16;
-  const int64_t units = B * Hkv * (hb > 0 ? hb : 1);
-  const int64_t target_waves = 4096;
-  int64_t st = (max_ctx * units + target_waves - 1) / target_waves;
-  const int64_t blk = 16 * kTilesPerBlock;
-  st = (st + blk - 1) / blk * blk;
-  if (st < 64) st = 64;
-  if (st > max_ctx) st = (max_ctx + blk - 1) / blk * blk;
-  return (int)st;
+inline int ilog2(int64_t v) {
+  int l = 0;
+  while ((int64_t(1) << l) < v) ++l;
+  return l;
+}
+inline bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+// Streaming multiprocessors (CUs) of the current device, cached per device.
+inline int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
 }
 
-inline bool fast_ok(int64_t D, int kvf, int dtype, int64_t gs) {
+inline bool fast_ok(int64_t D, int kvf, int dtype, int64_t gs, int64_t P, int64_t NP, int64_t Hkv) {
   if (!(D == 64 || D == 128)) return false;
+  if (!is_pow2(P) || (kMaxSplitPages - 1) * P < kBlockPos) return false;
+  if (NP * P * Hkv >= (int64_t(1) << 31)) return false;  // 32-bit row index
   if (kvf != 0) {
     if (dtype != MK_DT_F16) return false;
-    // one scale per 8 (K) / per lane's d-run (V): group must cover them
-    if (gs < 8 || (gs & (gs - 1))) return false;
+    // one scale per 8-d chunk: the group must be a power of two >= 8
+    if (gs < 8 || !is_pow2(gs)) return false;
   }
   return true;
 }
 
+// Host half of the split plan: workgroup shape, pairs aimed for (one per
+// resident workgroup slot: two waves per SIMD, four SIMDs per CU), the
+// longest split, and the pair count bound the workspace is sized for.
+inline void split_plan(PagedArgs& a) {
+  a.units = a.Hkv * a.HB;
+  // resident waves per round: two per SIMD, four SIMDs per CU
+  int64_t T = (int64_t)device_cus() * 8 / a.units;
+  if (T < 1) T = 1;
+  a.T_pairs = (int)T;
+  // pages one split may touch: 64 (one per lane) when tiles sit inside
+  // pages, else the LDS table's size
+  const int64_t max_pages = (a.P % 16 == 0) ? 64 : kMaxSplitPages;
+  int64_t cap = ((max_pages - 1) * a.P) / kBlockPos * kBlockPos;
+  if (cap < kBlockPos) cap = kBlockPos;
+  a.cap_tok = (int)cap;
+  // The device plan uses N <= r T pairs with r the smallest count of rounds,
+  // at least max(B/T + 1, MK_ATTN_ROUNDS), whose split fits the cap: either
+  // r is that floor (r T <= B + T or MK_ATTN_ROUNDS T) or the split at r - 1
+  // exceeded the cap, (r-1) T - B < total / cap, so r T < B max_ctx / cap + B + T.
+  const int64_t max_ctx = (int64_t)a.MB * a.P;
+  const int64_t by_cap = ((int64_t)a.B * max_ctx + cap - 1) / cap;
+  // (the minimum-split lowering only shrinks N; an all-empty batch uses B + 1)
+  a.max_pairs = (int)(T + by_cap + a.B + (int64_t)MK_ATTN_ROUNDS * T);
+}
+
+// Workspace: [O partials, max_pairs * Hq * D fp32][(m, l), max_pairs * Hq * 2 fp32]
+inline size_t workspace_need(const PagedArgs& a, int64_t D) {
+  return (size_t)a.max_pairs * a.Hq * (D + 2) * sizeof(float);
+}
+
 int attention_launch(PagedArgs a, int64_t D, int kvf, int dtype, size_t ws_bytes,
                      hipStream_t st) {
-  const int64_t max_ctx = (int64_t)a.MB * a.P;
-  a.split_tok = choose_split_tokens(a.B, a.Hq, a.Hkv, max_ctx);
-  a.s_max = (int)((max_ctx + a.split_tok - 1) / a.split_tok);
-  if (a.s_max < 1) a.s_max = 1;
-  const bool fast = fast_ok(D, kvf, dtype, a.gs);
-  if (fast && a.s_max > 1) {
-    const size_t need = (size_t)a.B * a.Hq * a.s_max * (D + 2) * sizeof(float);
-    if (!a.ws || ws_bytes < need) return MK_ERR_INVALID;
-  }
+  const bool fast = fast_ok(D, kvf, dtype, a.gs, a.P, a.NP, a.Hkv);
   if (fast) {
-    const dim3 grid((unsigned)a.s_max, (unsigned)(a.Hkv * a.HB), (unsigned)a.B);
-#define MK_PA(AT, DD, KF) paged_attn_kernel<AT, DD, KF><<<grid, 64, 0, st>>>(a)
+    a.lgP = ilog2(a.P);
+    a.lg_gs = kvf ? ilog2(a.gs) : 0;
+    split_plan(a);
+    const size_t need = workspace_need(a, D);
+    if (!a.ws || ws_bytes < need || !mk_aligned(a.ws, 16)) return MK_ERR_INVALID;
+      a.ws_ml = a.ws + (size_t)a.max_pairs * a.Hq * D;
+    const dim3 grid((unsigned)((int64_t)a.max_pairs * a.units));
+    const dim3 block(64u);
+#define MK_PA2(AT, DD, KF, SB)                                                        \
+  do {                                                                               \
+    if (a.P % 16 == 0) paged_attn_kernel<AT, DD, KF, SB, true><<<grid, block, 0, st>>>(a); \
+    else paged_attn_kernel<AT, DD, KF, SB, false><<<grid, block, 0, st>>>(a);       \
+  } while (0)
+#define MK_PA(AT, DD, KF, SB) MK_PA2(AT, DD, KF, SB)
     if (kvf == 0) {
       if (dtype == MK_DT_F16) {
-        if (D == 128) MK_PA(f16, 128, 0); else MK_PA(f16, 64, 0);
+        if (D == 128) MK_PA(f16, 128, 0, false); else MK_PA(f16, 64, 0, false);
       } else {
-        if (D == 128) MK_PA(bf16, 128, 0); else MK_PA(bf16, 64, 0);
+        if (D == 128) MK_PA(bf16, 128, 0, false); else MK_PA(bf16, 64, 0, false);
       }
     } else if (kvf == 8) {
-      if (D == 128) MK_PA(f16, 128, 8); else MK_PA(f16, 64, 8);
+      // SB: one K scale per 16-code run (group >= 16)
+      if (D == 128) {
+        if (a.gs >= 16) MK_PA(f16, 128, 8, true); else MK_PA(f16, 128, 8, false);
+      } else {
+        if (a.gs >= 16) MK_PA(f16, 64, 8, true); else MK_PA(f16, 64, 8, false);
+      }
     } else {
-      if (D == 128) MK_PA(f16, 128, 4); else MK_PA(f16, 64, 4);
+      // SB: one K scale per 32-code (D=128) / 16-code (D=64) run
+      if (D == 128) {
+        if (a.gs >= 32) MK_PA(f16, 128, 4, true); else MK_PA(f16, 128, 4, false);
+      } else {
+        if (a.gs >= 16) MK_PA(f16, 64, 4, true); else MK_PA(f16, 64, 4, false);
+      }
     }
 #undef MK_PA
+#undef MK_PA2
     MK_CHECK_LAUNCH();
-    if (a.s_max > 1) {
-      const dim3 mgrid((unsigned)(a.B * a.Hq));
-      if (dtype == MK_DT_F16)
-        paged_attn_merge_kernel<f16><<<mgrid, 64, 0, st>>>(a, (int)D);
-      else
-        paged_attn_merge_kernel<bf16><<<mgrid, 64, 0, st>>>(a, (int)D);
-      MK_CHECK_LAUNCH();
+    const dim3 mgrid((unsigned)((int64_t)a.B * a.Hq));
+    if (dtype == MK_DT_F16) {
+      if (D == 128) paged_attn_merge_kernel<f16, 128><<<mgrid, 64, 0, st>>>(a);
+      else paged_attn_merge_kernel<f16, 64><<<mgrid, 64, 0, st>>>(a);
+    } else {
+      if (D == 128) paged_attn_merge_kernel<bf16, 128><<<mgrid, 64, 0, st>>>(a);
+      else paged_attn_merge_kernel<bf16, 64><<<mgrid, 64, 0, st>>>(a);
     }
+    MK_CHECK_LAUNCH();
     return MK_OK;
   }
   if (D > 256) return MK_ERR_UNSUPPORTED;
@@ -585,11 +1071,18 @@ extern "C" {
 size_t mk_paged_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
                                           int64_t max_blocks, int64_t page_size) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_blocks <= 0 || page_size <= 0) return 0;
-  const int64_t max_ctx = max_blocks * page_size;
-  const int st = choose_split_tokens(B, Hq, Hkv, max_ctx);
-  const int64_t s_max = (max_ctx + st - 1) / st;
-  if (s_max <= 1) return 0;
-  return (size_t)B * Hq * s_max * (D + 2) * sizeof(float);
+  if (max_blocks * page_size >= (int64_t(1) << 31) || B >= 65536 || Hq >= (int64_t(1) << 24))
+    return 0;
+  PagedArgs a = {};
+  a.B = (int)B;
+  a.Hq = (int)Hq;
+  a.Hkv = (int)Hkv;
+  a.G = (int)(Hq / Hkv);
+  a.HB = (a.G + 15) / 16;
+  a.P = (int)page_size;
+  a.MB = (int)max_blocks;
+  split_plan(a);
+  return workspace_need(a, D);
 }
 
 int mk_paged_decode_attention(const void* q, const void* K_pages, const void* V_pages,

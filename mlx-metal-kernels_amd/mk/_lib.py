@@ -163,3 +163,13 @@ def launch(name: str, device: torch.device, *args) -> int:
 
 def workspace_bytes(B: int, Hq: int, Hkv: int, D: int, max_blocks: int, page_size: int) -> int:
     return int(load().mk_paged_attention_workspace_bytes(B, Hq, Hkv, D, max_blocks, page_size))
+
+
+def attention_workspace(device: torch.device, B: int, Hq: int, Hkv: int, D: int, max_blocks: int,
+                        page_size: int):
+    """(scratch, nbytes) for one paged-attention call: split partials, no
+    initial contents needed (None when the call needs none)."""
+    nbytes = workspace_bytes(B, Hq, Hkv, D, max_blocks, page_size)
+    if nbytes <= 0:
+        return None, 0
+    return torch.empty((nbytes + 15) // 16 * 16, dtype=torch.uint8, device=device), nbytes

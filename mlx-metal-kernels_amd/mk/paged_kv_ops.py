@@ -251,8 +251,7 @@ def _hip_paged_attention(q3, K_pages, V_pages, block_table, lengths, scale: floa
     bt = _i32(block_table, dev)
     ln = _i32(lengths, dev)
     out = torch.empty((B, Hq, D), dtype=dtype, device=dev)
-    ws_bytes = _lib.workspace_bytes(B, Hq, Hkv, D, MAX_BLOCKS, PAGE_SIZE)
-    ws = torch.empty((max(ws_bytes, 4) // 4,), dtype=torch.float32, device=dev) if ws_bytes else None
+    ws, ws_bytes = _lib.attention_workspace(dev, B, Hq, Hkv, D, MAX_BLOCKS, PAGE_SIZE)
     _lib.launch("mk_paged_decode_attention", dev, _lib.ptr(q3), _lib.ptr(Kp), _lib.ptr(Vp), _lib.ptr(bt),
                 _lib.ptr(ln), _lib.ptr(out), B, Hq, Hkv, D, PAGE_SIZE, MAX_BLOCKS, NUM_PAGES, float(scale),
                 _lib.dtype_code(dtype), _lib.ptr(ws), ws_bytes)

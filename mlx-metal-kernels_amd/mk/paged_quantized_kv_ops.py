@@ -378,8 +378,7 @@ def _hip_quantized_attention(q, paged_qkv: PagedQuantizedKVCache, lengths_arr, s
     bt = _i32(paged_qkv.block_table, dev)
     ln = _i32(lengths_arr, dev)
     out = torch.empty((B, Hq, D), dtype=q.dtype, device=dev)
-    ws_bytes = _lib.workspace_bytes(B, Hq, Hkv, D, MAX_BLOCKS, PAGE_SIZE)
-    ws = torch.empty((max(ws_bytes, 4) // 4,), dtype=torch.float32, device=dev) if ws_bytes else None
+    ws, ws_bytes = _lib.attention_workspace(dev, B, Hq, Hkv, D, MAX_BLOCKS, PAGE_SIZE)
     _lib.launch("mk_paged_quantized_decode_attention", dev, _lib.ptr(q3), _lib.ptr(kq), _lib.ptr(vq), _lib.ptr(ks),
                 _lib.ptr(vs), _lib.ptr(bt), _lib.ptr(ln), _lib.ptr(out), B, Hq, Hkv, D, PAGE_SIZE, MAX_BLOCKS,
                 NUM_PAGES, paged_qkv.group_size, paged_qkv.bits, float(scale), _lib.dtype_code(q.dtype),

@@ -87,6 +87,14 @@ ATTN_CASES = [
     (2, 4, 2, 16, 4, 8),
     (2, 2, 1, 96, 8, 6),
     (1, 3, 3, 17 * 2, 4, 4),
+    # 12 kv heads: two workgroups per (sequence, split), the second half full
+    (3, 24, 12, 128, 16, 30),
+    # MQA, 32 query heads on one kv head: two 16-head column blocks
+    (2, 32, 1, 64, 32, 12),
+    # page size 64: tiles inside pages, splits not page-aligned
+    (2, 8, 2, 128, 64, 40),
+    # many sequences: the pair scan spans several 64-lane chunks
+    (130, 8, 2, 64, 16, 3),
 ]
 
 

@@ -33,12 +33,12 @@ HEADER = os.path.join(ROOT, "include", "mk_hip.h")
 
 
 def _header_decls():
-    """{name: parameter count} for every ``int|size_t mk_*(...)`` declaration."""
+    """{name: parameter count} for every ``int|int64_t|size_t mk_*(...)`` declaration."""
     text = open(HEADER).read()
     text = re.sub(r"//[^\n]*", "", text)
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     out = {}
-    for m in re.finditer(r"\b(?:int|size_t)\s+(mk_\w+)\s*\(([^)]*)\)\s*;", text):
+    for m in re.finditer(r"\b(?:int|int64_t|size_t)\s+(mk_\w+)\s*\(([^)]*)\)\s*;", text):
         params = m.group(2).strip()
         out[m.group(1)] = 0 if params in ("", "void") else len(params.split(","))
     return out
@@ -71,6 +71,7 @@ def test_abi_version_and_workspace():
     ws = _lib.workspace_bytes(16, 32, 8, 128, 512, 16)
     assert ws > 0 and ws % 4 == 0
     assert _lib.workspace_bytes(1, 8, 8, 64, 1, 16) >= 0
+
 
 
 def test_invalid_arguments_are_rejected_on_the_host():
