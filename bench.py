@@ -36,6 +36,9 @@ sys.path.insert(0, os.path.join(ROOT, "mlx-metal-kernels_amd"))
 
 PEAK_GBS = 8000.0
 HIDDEN, INTER, GROUP = 4096, 14336, 64
+DOMINANT_KERNEL = "gemv_dot_kernel<4, 2, 2>"  # q4 gate/up + SwiGLU at M = 1
+COPY_KERNEL_HINT = "copy"                      # torch's device-to-device copy kernel
+TRAFFIC_SUMMARY = "gemv_dot_q4_gate_up_M1_traffic.json"
 
 
 def _parse():
@@ -46,6 +49,12 @@ def _parse():
     ap.add_argument("--sets", type=int, default=6, help="distinct weight sets rotated through (>= 512 MB total)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the M=4/8, q8 and attention extras")
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="first run a plain device copy of this many MiB (counter calibration)")
+    ap.add_argument("--summarize-counters", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE run, "
+                         "WRITE_SIZE run, both with --calib-copy-mb) into the traffic summary and exit")
+    ap.add_argument("--summary-out", default=os.path.join(ROOT, "profiles", TRAFFIC_SUMMARY))
     return ap.parse_args()
 
 
@@ -250,11 +259,66 @@ def cpu_baseline(sets, x_res_nw, budget_s=20.0):
     return med, len(times), blas
 
 
+# ----------------------------------------------------------------- counters
+
+
+def _counter_rows(path, counter):
+    import csv
+
+    rows = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if r.get("Counter_Name") == counter:
+                rows.append((r.get("Kernel_Name", ""), float(r["Counter_Value"])))
+    return rows
+
+
+def summarize_counters(fetch_csv, write_csv, out_path, copy_mb):
+    """HBM traffic per launch of the dominant kernel from FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch), each scaled by what the same counter reads
+    for the plain copy of ``copy_mb`` MiB run by --calib-copy-mb."""
+    copy_bytes = copy_mb * (1 << 20)
+    out = {"kernel": DOMINANT_KERNEL, "workload": "config2 gate/up 2x14336x4096 q4 g64 M=1",
+           "algorithmic_bytes": None, "copy_bytes": copy_bytes}
+    for name, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rows = _counter_rows(path, name)
+        dom = [v for k, v in rows if DOMINANT_KERNEL in k.replace("(anonymous namespace)::", "")]
+        cop = [v for k, v in rows if COPY_KERNEL_HINT in k.lower() and "gemv" not in k]
+        if not dom or not cop:
+            raise SystemExit(f"{name}: kernel rows not found in {path}")
+        # the calibration copy reads and writes copy_bytes once each; take its
+        # largest dispatch (the one of the known size)
+        factor = copy_bytes / (max(cop) * 1024.0)
+        per_launch_kib = sum(dom) / len(dom)
+        out[name] = {"kib_per_dispatch": round(per_launch_kib, 1), "dispatches": len(dom),
+                     "copy_kib": round(max(cop), 1), "scale": round(factor, 4),
+                     "bytes_per_launch": int(per_launch_kib * 1024.0 * factor)}
+    out["traffic_bytes_per_launch"] = out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"]
+    b_gu, _, _ = mlp_bytes(1, 4)
+    out["algorithmic_bytes"] = b_gu
+    out["traffic_over_algorithmic"] = round(out["traffic_bytes_per_launch"] / b_gu, 4)
+    with open(out_path, "w") as f:
+        json.dump(out, f, indent=2)
+    print(json.dumps(out))
+
+
+def load_traffic():
+    """Measured HBM bytes per launch of the dominant kernel (profiles/), or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", TRAFFIC_SUMMARY)) as f:
+            return int(json.load(f)["traffic_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 # ----------------------------------------------------------------- main
 
 
 def main():
     args = _parse()
+    if args.summarize_counters:
+        summarize_counters(*args.summarize_counters, args.summary_out, args.calib_copy_mb or 256)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one GPU; multi-GPU runs are not part of it",
                           "requested_gpus": args.gpus}))
@@ -266,6 +330,13 @@ def main():
     dev = torch.device("cuda:0")
     _lib.load()
     torch.manual_seed(0)
+    if args.calib_copy_mb:
+        src = torch.empty(args.calib_copy_mb << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     sets = [make_mlp_set(dev, 4, 100 + i) for i in range(args.sets)]
     set_bytes = sum(t.numel() * t.element_size() for ws in sets for m in ws for t in m)
@@ -328,7 +399,7 @@ def main():
                    "group_size": GROUP, "M": 1, "weight_sets": args.sets, "weight_set_bytes_total": set_bytes,
                    "step_bytes": step_bytes, "frac_of_peak": round(value / PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": load_traffic(),
                      "kernel": "gemv_dot_kernel<4,2,2> q4 gate/up+SwiGLU 2x14336x4096 M=1",
                      "bytes_per_launch": b_gu, "us_per_launch": round(ms_gu * 1e3, 3)},
         "cpu_baseline": cpu,
