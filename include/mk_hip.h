@@ -65,6 +65,15 @@ int mk_dequant_q4(const uint8_t* packed, const void* scales, const void* zeros, 
 int mk_dequant_q8(const uint8_t* q, const void* scales, const void* zeros, void* out, int64_t rows,
                   int64_t K, int64_t group_size, int scale_dtype, int out_dtype, void* stream);
 
+/* quantize_weight_groupwise -- models/quantize_weights.py:164-203 (symmetric):
+ * weight [rows, K] (fp32/fp16/bf16) -> codes uint8 [rows, ceil(K/2)] (q4,
+ * low nibble = even k, odd K padded with 0) or [rows, K] (q8), and scales
+ * [rows, ceil(K/g)] in scale_dtype.  scale = max(max|w| / (7|127), eps) in
+ * double, codes = clip(rint(w / float(scale)), -limit, limit) + 8|128. */
+int mk_quantize_weight(const void* weight, uint8_t* codes, void* scales, int64_t rows, int64_t K,
+                       int64_t group_size, int bits, double eps, int w_dtype, int scale_dtype,
+                       void* stream);
+
 /* ---------------------------------------------------------------- quantized matvec family */
 
 /* q4_matvec_decode -- ops/quant_ops.py:529-571 (all four backends:

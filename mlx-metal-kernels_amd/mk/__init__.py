@@ -18,6 +18,7 @@ __all__ = [
     "norm_ops",
     "paged_kv_ops",
     "paged_quantized_kv_ops",
+    "quantize_weights",
     "quant_ops",
     "rope_ops",
 ]

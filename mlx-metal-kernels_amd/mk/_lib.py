@@ -38,6 +38,7 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I = ctypes.c_int
 _F = ctypes.c_float
+_D = ctypes.c_double
 _SZ = ctypes.c_size_t
 
 # name -> argtypes (restype int unless listed in _RESTYPES)
@@ -47,6 +48,7 @@ SIGNATURES: dict[str, list] = {
     "mk_unpack_q4": [_P, _P, _I64, _I64, _I64, _P],
     "mk_dequant_q4": [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P],
     "mk_dequant_q8": [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P],
+    "mk_quantize_weight": [_P, _P, _P, _I64, _I64, _I64, _I, _D, _I, _I, _P],
     "mk_q4_matvec": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P],
     "mk_q8_matvec": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P],
     "mk_q4_gate_up": [_P] * 10 + [_I64] * 4 + [_I, _I, _P],

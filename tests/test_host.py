@@ -251,3 +251,39 @@ def test_ctypes_pointer_helper():
     t = torch.zeros(4)
     assert _lib.ptr(t) == t.data_ptr()
     assert isinstance(ctypes.c_void_p(_lib.ptr(t)).value, int)
+
+
+# ------------------------------------------------------------------ weight quantizer (host paths)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("n,k,g", [(8, 64, 32), (5, 67, 64), (3, 33, 7), (4, 4096, 64)])
+def test_weight_quantizer_reference_backend_matches_oracle(bits, n, k, g):
+    import mk.quantize_weights as qw
+
+    rng = np.random.default_rng(bits * 1000 + k + g)
+    W = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    W[0, :g] = 0.0  # an all-zero group: scale = eps
+    r = qw.quantize_weight_groupwise(torch.from_numpy(W), qw.QuantizationConfig(bits=bits, group_size=g,
+                                                                                 dtype="float32"),
+                                     backend="reference")
+    p, s = oq.quantize_weight_groupwise(W, bits, g)
+    assert np.array_equal(r.packed_weight.numpy(), p)
+    assert np.array_equal(r.scales.numpy().view(np.uint32), s.view(np.uint32))
+    assert r.zeros is None and r.original_shape == (n, k)
+    assert torch.all(r.kernel_zeros() == (8.0 if bits == 4 else 128.0))
+
+
+def test_weight_quantizer_validation():
+    import mk.quantize_weights as qw
+
+    with pytest.raises(ValueError, match="bits must be 4 or 8"):
+        qw.QuantizationConfig(bits=3).validate()
+    with pytest.raises(ValueError, match="dtype must be one of"):
+        qw.QuantizationConfig(dtype="int8").validate()
+    with pytest.raises(NotImplementedError):
+        qw.quantize_weight_groupwise(torch.zeros(2, 4), qw.QuantizationConfig(symmetric=False))
+    with pytest.raises(ValueError, match="rank-2"):
+        qw.quantize_weight_groupwise(torch.zeros(4), qw.QuantizationConfig())
+    with pytest.raises(ValueError, match="ROCm device"):
+        qw.quantize_weight_groupwise(torch.zeros(2, 64), qw.QuantizationConfig())
