@@ -397,9 +397,30 @@ constexpr int dot_rows() {
   return (BITS == 8 && NMAT == 2) ? 4 : 8;
 }
 constexpr int DOT_SZ_VEC = 2;  // 16-byte (s|z) vectors staged per lane
+constexpr int SEG_STRIDE = 64; // fp16 entries per staged (s|z) run
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(bitcast<f16x2>(a), bitcast<f16x2>(b), c, false);
+}
+
+// Partner exchange at lane distance D for the reductions below.  D = 32 and
+// 16 use the gfx950 permlane swaps: permlane32_swap(a, b) leaves a = (a.lo,
+// b.lo) and b = (a.hi, b.hi) by 32-lane halves, permlane16_swap does the same
+// for the odd/even 16-lane rows, so a + b holds, in lanes with bit D clear,
+// the pair sum of a and, in lanes with bit D set, the pair sum of b.  Smaller
+// distances use ds_swizzle in bitmask mode (xor within 32 lanes).
+template <int D>
+__device__ __forceinline__ float swap_sum(float a, float b) {
+  static_assert(D == 32 || D == 16, "permlane swaps cover D = 32, 16");
+  const auto r = D == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false)
+                         : __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int D>
+__device__ __forceinline__ float xor_lane(float v) {
+  static_assert(D >= 1 && D <= 16, "swizzle xor covers D < 32");
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (D << 10) | 0x1F));
 }
 
 // Butterfly that halves the live values per step: at distance d a lane keeps
@@ -412,16 +433,22 @@ __device__ __forceinline__ void reduce_scatter(float* v, int lane) {
   if constexpr (D >= 1) {
     if constexpr (CNT > 1) {
       constexpr int H = CNT / 2;
-      const bool upper = (lane & D) != 0;
+      if constexpr (D >= 16) {
 #pragma unroll
-      for (int j = 0; j < H; ++j) {
-        const float keep = upper ? v[j + H] : v[j];
-        const float send = upper ? v[j] : v[j + H];
-        v[j] = keep + __shfl_xor(send, D, 64);
+        for (int j = 0; j < H; ++j) v[j] = swap_sum<D>(v[j], v[j + H]);
+      } else {
+        const bool upper = (lane & D) != 0;
+#pragma unroll
+        for (int j = 0; j < H; ++j) {
+          const float keep = upper ? v[j + H] : v[j];
+          const float send = upper ? v[j] : v[j + H];
+          v[j] = keep + xor_lane<D>(send);
+        }
       }
       reduce_scatter<H, D / 2>(v, lane);
     } else {
-      v[0] += __shfl_xor(v[0], D, 64);
+      if constexpr (D >= 16) v[0] = swap_sum<D>(v[0], v[0]);
+      else v[0] += xor_lane<D>(v[0]);
       reduce_scatter<1, D / 2>(v, lane);
     }
   }
@@ -438,6 +465,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     const GemvArgs args) {
   constexpr int R = dot_rows<BITS, NMAT>();
   constexpr int V = NMAT * R;  // values reduced per lane
+  constexpr int NSEG = V * 2;  // (matrix, row, s|z) runs staged per wave
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int kw = args.kw;
@@ -457,8 +485,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
   const int U = K / 32;
   // branch-free: a lane past the last unit re-reads unit 0 (its sums are
   // dropped), so all loads sit in one block and vmcnt waits stay exact
+  // x goes out before the codes: vmcnt retires in issue order, so the x
+  // operands are ready after the first waits and row (t, r) computes as soon
+  // as its own code load has landed, overlapping the loads still in flight
   auto load = [&](int u, DotFrag<BITS, NMAT, R>& f) {
     const int k0 = (u < U ? u : 0) * 32;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.x[j] = ldg128(x + k0 + 8 * j);
 #pragma unroll
     for (int t = 0; t < NMAT; ++t)
 #pragma unroll
@@ -467,44 +500,44 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
         f.w[t][r][0] = ldg128_stream(p);
         if constexpr (BITS == 8) f.w[t][r][BITS == 4 ? 0 : 1] = ldg128_stream(p + 16);
       }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) f.x[j] = ldg128(x + k0 + 8 * j);
   };
 
   // Scales and zero points: each wave stages, in its own LDS region, the
-  // (s, z) of its rows for the groups its 64 units cover -- NMAT*R*2
-  // contiguous runs of gpw fp16 values, fetched with 128-bit loads.  They are
-  // requested first, then the code loads go out, then the LDS writes (vmcnt is
-  // in order: the writes wait for the small loads only, the code loads stay in
-  // flight).  No workgroup barrier is needed: LDS ops of a wave run in order.
-  const int gpw = 2048 >> args.lg;  // groups per 64-unit slice
-  const int nseg = NMAT * R * 2;    // (matrix, row, s|z) runs
-  const int seg_vec = gpw / 8;      // 16-byte vectors per run
-  const int nvec = nseg * seg_vec;  // <= 64 * DOT_SZ_VEC
-  __shared__ u32x4 szw[8][64 * DOT_SZ_VEC];
+  // (s, z) of its rows for the groups its 64 units cover -- NSEG runs of gpw
+  // fp16 values (gpw <= 64), fetched with 128-bit loads and stored at a fixed
+  // stride of 64 entries so a row's run sits at a compile-time offset.  They
+  // are requested first, then x and the codes, then the LDS writes (vmcnt is
+  // in order: the writes wait for the small loads only).  No workgroup barrier
+  // is needed: LDS ops of a wave run in order.
+  const int lsv = 8 - args.lg;      // log2(16-byte vectors per run), gpw = 8 << lsv
+  const int nvec = NSEG << lsv;     // <= 64 * DOT_SZ_VEC (checked by the dispatcher)
+  extern __shared__ __align__(16) uint8_t dot_stage[];  // kw * NSEG * 128 bytes
+  uint8_t* stage = dot_stage + wave * (NSEG * 2 * SEG_STRIDE);
   u32x4 szv[DOT_SZ_VEC];
-  bool sz_zero[DOT_SZ_VEC];
-  int ubase = wave * 64;
+  uint32_t sz_zero[DOT_SZ_VEC];
+  const int ubase = wave * 64;
   {
     // branch-free: lanes without a run (or a missing zero tensor) read a valid
-    // dummy vector and drop it, so every load counts in order for vmcnt
+    // vector of the same row and drop it, so every load counts in order for
+    // vmcnt.  A partial last slice clamps its vectors to the row's last 8
+    // groups: the units past K that would use them are dropped.
     const int g0 = (ubase * 32) >> args.lg;
     const f16* s0 = reinterpret_cast<const f16*>(args.s[0]);
     const f16* s1 = reinterpret_cast<const f16*>(args.s[NMAT - 1]);
     const f16* z0 = args.z[0] ? reinterpret_cast<const f16*>(args.z[0]) : s0;
     const f16* z1 = args.z[NMAT - 1] ? reinterpret_cast<const f16*>(args.z[NMAT - 1]) : s1;
-    const bool has_z = args.z[0] != nullptr;
+    const uint32_t has_z = args.z[0] != nullptr ? 1u : 0u;
 #pragma unroll
     for (int j = 0; j < DOT_SZ_VEC; ++j) {
       const int v = lane + 64 * j;
-      const bool use = v < nvec && ubase < U;
-      const int seg = use ? v / seg_vec : 0;
-      const int e = use ? v - seg * seg_vec : 0;
+      const int vv = v < nvec ? v : 0;
+      const int seg = vv >> lsv;
+      const int e = vv & ((1 << lsv) - 1);
       const int t = seg / (2 * R), r = (seg >> 1) % R, isz = seg & 1;
       const f16* base = t == 0 ? (isz ? z0 : s0) : (isz ? z1 : s1);
       const int nr = min(n0 + r, N - 1);
-      szv[j] = ldg128(base + (size_t)nr * G + g0 + 8 * e);
-      sz_zero[j] = isz && !has_z;  // zero tensor absent: z = 0 (applied at the LDS write)
+      szv[j] = ldg128(base + (size_t)nr * G + min(g0 + 8 * e, G - 8));
+      sz_zero[j] = (uint32_t)isz & (has_z ^ 1u);  // zero tensor absent: z = 0
     }
   }
   __builtin_amdgcn_sched_barrier(0);  // keep the small loads ahead of the code loads
@@ -512,10 +545,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
   load(ubase + lane, f);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int j = 0; j < DOT_SZ_VEC; ++j)
-    szw[wave][lane + 64 * j] = sz_zero[j] ? (u32x4){0u, 0u, 0u, 0u} : szv[j];
+  for (int j = 0; j < DOT_SZ_VEC; ++j) {
+    const int v = lane + 64 * j;
+    if (v < nvec) {
+      const int seg = v >> lsv, e = v & ((1 << lsv) - 1);
+      *reinterpret_cast<u32x4*>(stage + seg * (2 * SEG_STRIDE) + e * 16) =
+          sz_zero[j] ? (u32x4){0u, 0u, 0u, 0u} : szv[j];
+    }
+  }
   __builtin_amdgcn_wave_barrier();
-  const f16* szl = reinterpret_cast<const f16*>(&szw[wave][0]);
 
   float acc[V];
 #pragma unroll
@@ -523,14 +561,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
 
   {  // one 64-unit slice per wave (the dispatcher guarantees U <= 64 * kw)
     const int u = ubase + lane;
-    const bool valid = u < U;
-    const int k0 = valid ? u * 32 : 0;
+    // a lane past the last unit computes on x = 0: its codes, offsets and
+    // zero-point terms all vanish, so its sums add nothing
+    if (u >= U) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) f.x[j] = (u32x4){0u, 0u, 0u, 0u};
+    }
 
     // activation operands in the unpack order, and their sums
     uint32_t xp[16];
-    float xs_hi = 0.0f, xs = 0.0f;  // X_hi and X
+    float xs = 0.0f;  // X, the sum of the slice's x
+    float boff;       // what the exponent-magic offsets add to the code sums
     const uint32_t one2 = 0x3C003C00u;  // (1.0h, 1.0h)
     if constexpr (BITS == 4) {
+      // low nibbles decode to 1024 + c, high nibbles (in place) to
+      // 1024 + 16 c against x / 16: the offsets sum to 1024 X_lo + 64 X_hi
+      float xs_hi = 0.0f, xs_lo = 0.0f;
       const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -540,13 +586,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
         const uint32_t p2 = pack_lo16(f.x[j][1], f.x[j][3]);
         const uint32_t p3 = pack_hi16(f.x[j][1], f.x[j][3]);
         xs_hi = dot2(p1, one2, dot2(p3, one2, xs_hi));
-        xs = dot2(p0, one2, dot2(p2, one2, xs));
+        xs_lo = dot2(p0, one2, dot2(p2, one2, xs_lo));
         xp[4 * j + 0] = p0;
         xp[4 * j + 1] = bitcast<uint32_t>(bitcast<f16x2>(p1) * sixteenth);
         xp[4 * j + 2] = p2;
         xp[4 * j + 3] = bitcast<uint32_t>(bitcast<f16x2>(p3) * sixteenth);
       }
-      xs += xs_hi;
+      xs = xs_lo + xs_hi;
+      boff = 1024.0f * xs_lo + 64.0f * xs_hi;
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -558,26 +605,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
         xs = dot2(xp[4 * j + 0], one2, dot2(xp[4 * j + 1], one2,
                   dot2(xp[4 * j + 2], one2, dot2(xp[4 * j + 3], one2, xs))));
       }
+      boff = 1024.0f * xs;
     }
-    const float boff = BITS == 4 ? 64.0f * xs_hi : 1024.0f * xs;
-    const int gl = (lane * 32) >> args.lg;  // group within this wave's slice
+    const float nboff = -boff;
+    // this lane's group within the wave's slice; run seg is at seg * 64
+    const f16* szl = reinterpret_cast<const f16*>(stage) + ((lane * 32) >> args.lg);
 
 #pragma unroll
     for (int t = 0; t < NMAT; ++t)
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        float tsum = 0.0f;
+        float tsum = nboff;
         if constexpr (BITS == 4) {
-          const f16x2 k1024 = {(f16)1024.0f, (f16)1024.0f};
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             const uint32_t q = f.w[t][r][0][w];
             const uint32_t v = q >> 8;
-            const uint32_t c04 = bitcast<uint32_t>(bitcast<f16x2>((q & 0x000F000Fu) | magic) - k1024);
-            const uint32_t c26 = bitcast<uint32_t>(bitcast<f16x2>((v & 0x000F000Fu) | magic) - k1024);
-            tsum = dot2(c04, xp[4 * w + 0], tsum);
+            tsum = dot2((q & 0x000F000Fu) | magic, xp[4 * w + 0], tsum);
             tsum = dot2((q & 0x00F000F0u) | magic, xp[4 * w + 1], tsum);
-            tsum = dot2(c26, xp[4 * w + 2], tsum);
+            tsum = dot2((v & 0x000F000Fu) | magic, xp[4 * w + 2], tsum);
             tsum = dot2((v & 0x00F000F0u) | magic, xp[4 * w + 3], tsum);
           }
         } else {
@@ -589,12 +635,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
           }
         }
         const int seg = (t * R + r) * 2;
-        const float sv = (float)szl[seg * gpw + gl];
-        const float zv = (float)szl[(seg + 1) * gpw + gl];
-        const float term = sv * (tsum - boff - zv * xs);
-        acc[t * R + r] += valid ? term : 0.0f;
+        const float sv = (float)szl[seg * SEG_STRIDE];
+        const float zv = (float)szl[(seg + 1) * SEG_STRIDE];
+        acc[t * R + r] = fmaf(sv, fmaf(-zv, xs, tsum), acc[t * R + r]);
       }
-
   }
 
   // ---- 64-lane reduction (halving butterfly), then across waves in LDS
@@ -706,7 +750,8 @@ template <int BITS, int NMAT, int EPI>
 int launch_dot(const GemvArgs& a, hipStream_t st) {
   constexpr int R = dot_rows<BITS, NMAT>();
   const dim3 grid((a.N + R - 1) / R);
-  gemv_dot_kernel<BITS, NMAT, EPI><<<grid, dim3(64 * a.kw), 0, st>>>(a);
+  const size_t stage_bytes = (size_t)a.kw * NMAT * R * 2 * (2 * SEG_STRIDE);
+  gemv_dot_kernel<BITS, NMAT, EPI><<<grid, dim3(64 * a.kw), stage_bytes, st>>>(a);
   MK_CHECK_LAUNCH();
   return MK_OK;
 }

@@ -65,6 +65,11 @@ MATVEC_CASES = [
     (8, 4096, 14336, 64),
     (16, 96, 512, 128),
     (17, 64, 256, 64),
+    # M = 1 dot path with a partial last 2048-k slice (K % 2048 != 0)
+    (1, 200, 3072, 64),
+    (1, 77, 2560, 64),
+    (1, 96, 512, 64),
+    (1, 64, 5120, 32),
 ]
 
 
@@ -86,7 +91,7 @@ def test_matvec_f16(dev, bits, M, N, K, g):
 @pytest.mark.parametrize("act", ["f16", "bf16"])
 @pytest.mark.parametrize("zeros_kind", ["none", "affine"])
 @pytest.mark.parametrize("sdt", [torch.float16, torch.float32])
-@pytest.mark.parametrize("M,N,K,g", [(2, 50, 96, 16), (3, 40, 512, 64)])
+@pytest.mark.parametrize("M,N,K,g", [(2, 50, 96, 16), (3, 40, 512, 64), (1, 72, 3072, 64)])
 def test_matvec_dtypes_and_zeros(dev, bits, act, zeros_kind, sdt, M, N, K, g):
     rng = np.random.default_rng(7)
     codes, stored, s, z = quant_weight(rng, N, K, g, bits, zeros_kind, "normal")
@@ -118,7 +123,8 @@ def test_matvec_saturates(dev, bits):
 # ------------------------------------------------------------ gate / up / MLP
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("rows,N,K,g", [(3, 50, 96, 32), (1, 14336, 4096, 64), (8, 512, 4096, 64), (5, 64, 95, 32)])
+@pytest.mark.parametrize("rows,N,K,g", [(3, 50, 96, 32), (1, 14336, 4096, 64), (8, 512, 4096, 64), (5, 64, 95, 32),
+                                        (1, 300, 3072, 64)])
 def test_gate_up_and_swiglu_epilogue(dev, bits, rows, N, K, g):
     if bits == 8 and K % 2:
         pytest.skip("odd K only matters for the q4 ceil(K/2) packing")
