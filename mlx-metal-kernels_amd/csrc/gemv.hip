@@ -390,11 +390,13 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(const GemvArgs args) {
 // workgroup's rows are staged in LDS.  Needs fp16 activations, fp16 scales,
 // power-of-two group size >= 32, K % 32 == 0.
 // --------------------------------------------------------------------------
-// rows per workgroup (per matrix): 8, except q8 gate/up whose 32 code loads
-// per lane would not fit 4 waves/SIMD worth of registers
+// rows per workgroup (per matrix): 4 for gate/up (twice the workgroups of 8
+// rows keep more waves queued behind the resident ones, which shortens the
+// drain at the end of the launch), 8 for a single matrix (whose K-split over
+// up to 8 waves already gives each workgroup enough waves)
 template <int BITS, int NMAT>
 constexpr int dot_rows() {
-  return (BITS == 8 && NMAT == 2) ? 4 : 8;
+  return NMAT == 2 ? 4 : 8;
 }
 constexpr int DOT_SZ_VEC = 2;  // 16-byte (s|z) vectors staged per lane
 constexpr int SEG_STRIDE = 64; // fp16 entries per staged (s|z) run

@@ -124,7 +124,7 @@ def test_matvec_saturates(dev, bits):
 
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("rows,N,K,g", [(3, 50, 96, 32), (1, 14336, 4096, 64), (8, 512, 4096, 64), (5, 64, 95, 32),
-                                        (1, 300, 3072, 64)])
+                                        (1, 300, 3072, 64), (1, 256, 4096, 32)])
 def test_gate_up_and_swiglu_epilogue(dev, bits, rows, N, K, g):
     if bits == 8 and K % 2:
         pytest.skip("odd K only matters for the q4 ceil(K/2) packing")
