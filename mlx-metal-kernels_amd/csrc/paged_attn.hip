@@ -11,19 +11,21 @@
 //   with no position yields zeros.  Quantized K/V dequantize as
 //   (code - 128|8) * scale rounded to fp16, as dequantize_kv_pages does.
 //
-// Fast path (D in {64,128}, fp16 q for quantized caches): one wave per
-// (split of the context, kv head, sequence[, block of 16 query heads]).
+// Fast path (D in {64,128}, fp16 q for quantized caches): the 32-position
+// blocks of all sequences are cut into equal "pairs" (see the stream plan);
+// one wave per (pair, kv head[, block of 16 query heads]) streams its pair's
+// blocks, crossing sequence boundaries.
 //   QK^T : v_mfma_f32_16x16x32  A = K tile (16 positions x 32 d), loaded
 //          straight from the page (lane = position, 4 lanes cover one row),
 //          B = q^T (32 d x 16 heads; the GQA group fills the columns, so one
 //          K read serves all Hq/Hkv heads).
-//   P.V  : v_mfma_f32_16x16x16  A = P (16 heads x 16 positions) -- exactly the
-//          accumulator layout QK^T leaves behind, B = V tile regrouped per
-//          output column.
-// The online softmax runs in base 2 on 32-position blocks; splits write
-// (m, l, O) partials that a second kernel merges (LSE merge,
-// ops/attention_ops.py:534-550).  A sequence that fits one split is finished
-// in place.
+//   P.V  : v_mfma_f32_16x16x32  A = P (16 heads x 32 positions) -- exactly
+//          the accumulator layout QK^T leaves behind, B = V tile regrouped
+//          per output column.
+// The online softmax runs in base 2 on 32-position blocks; a sequence split
+// over several pairs gets (m, l, O) partials that a second kernel merges
+// (LSE merge, ops/attention_ops.py:534-550); one inside a single pair is
+// finished in place.
 #include "common.h"
 
 namespace {
@@ -32,16 +34,26 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kBlockPos = 32;         // positions per softmax block (two MFMA tiles)
 constexpr int kMaxSplitPages = 512;   // page ids one split may touch (LDS)
 
-// Shortest split (in 32-position blocks): below it a wave's fixed start-up
-// cost outweighs the extra parallelism.
+// Fewest 32-position blocks per pair: below it a wave's fixed start-up cost
+// outweighs the extra parallelism.
 #ifndef MK_ATTN_MIN_SPLIT_BLOCKS
-#define MK_ATTN_MIN_SPLIT_BLOCKS 8
+#define MK_ATTN_MIN_SPLIT_BLOCKS 4
 #endif
-// Rounds of resident waves the split plan aims for at least (measured: one
-// round is best -- later rounds pay their start-up loads at loaded latency).
-#ifndef MK_ATTN_ROUNDS
-#define MK_ATTN_ROUNDS 1
+// Segments per pair whose q is staged in LDS at start-up (a pair crossing
+// more sequences loads the rest when it reaches them).
+#ifndef MK_ATTN_QSLOTS
+#define MK_ATTN_QSLOTS 3
 #endif
+constexpr int kQSlots = MK_ATTN_QSLOTS;
+// Segments one pair may touch (one per block at most; the plan keeps a pair
+// within 64 blocks).
+constexpr int kMaxSegs = 64;
+
+// One segment of a pair: sequence, first and end position, page-list index
+// of its first page (bit 30: the segment is the whole sequence).
+struct SegDesc {
+  int b, t0, t1, po;
+};
 // MK_ATTN_NT 1 reads K/V pages with nontemporal loads (measured: no gain on
 // balance -- slightly faster for fp16 pages, slower for q8 -- so off).
 #ifndef MK_ATTN_NT
@@ -57,16 +69,18 @@ struct PagedArgs {
   const int32_t* bt;   // [B, MB]
   const int32_t* lengths;
   void* out;           // [B, Hq, D]
-  float* ws;           // split partials O: [max_pairs][Hq][D] fp32
-  float* ws_ml;        // split partials (m, l): [max_pairs][Hq][2] fp32
+  float* ws;           // partials O: [slots][Hq][D] fp32, slots = max_pairs + B
+  float* ws_ml;        // partials (m, l): [slots][Hq][2] fp32
   int B, Hq, Hkv, G, HB;
   int NP, P, MB, lgP;  // fast path: P = 1 << lgP
   int gs, ngroups;     // quantization group size and groups per head
   int lg_gs;           // fast path: gs = 1 << lg_gs
-  // fast-path split plan (see plan_pairs): (sequence, split) pairs per round,
-  // the longest split allowed, and the pair count the workspace can hold
-  int T_pairs, cap_tok, max_pairs;
+  // fast-path stream plan (see stream_plan): pairs per round of resident
+  // waves, the most blocks one pair may hold, and the pair count bound the
+  // workspace and the grid are sized for
+  int T_pairs, cap_blk, max_pairs;
   int units;           // (kv head, block of 16 query heads) waves per pair
+  int wg_units;        // units per workgroup (a divisor of units, <= 8)
   float scale_log2;
 };
 
@@ -81,17 +95,6 @@ template <>
 __device__ __forceinline__ f32x4 mfma_k32<bf16>(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(bitcast<bf16x8>(a), bitcast<bf16x8>(b), c, 0, 0,
                                                  0);
-}
-template <typename AT>
-__device__ __forceinline__ f32x4 mfma_k16(u32x2 a, u32x2 b, f32x4 c);
-template <>
-__device__ __forceinline__ f32x4 mfma_k16<f16>(u32x2 a, u32x2 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(bitcast<f16x4>(a), bitcast<f16x4>(b), c, 0, 0, 0);
-}
-template <>
-__device__ __forceinline__ f32x4 mfma_k16<bf16>(u32x2 a, u32x2 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bitcast<s16x4>(a), bitcast<s16x4>(b), c, 0, 0,
-                                                   0);
 }
 
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
@@ -241,23 +244,28 @@ struct KVBlock {
   uint32_t mask;  // bit p: position p of the block is valid (wave-uniform)
 };
 
-// ------------------------------------------------------------ split plan
-// The work is cut into N (sequence, split) pairs, N a whole number r of
-// rounds of T_pairs (one resident workgroup slot per pair), so that the
-// pairs fill the machine evenly whatever the lengths.  Sequence b gets
-//   n_b = 1 + floor((N-B) cum_b / total) - floor((N-B) cum_{b-1} / total)
-// pairs (cum = inclusive prefix of the lengths): at least one, the rest in
-// proportion to its length, sum exactly N.  Its splits are
-// st_b = ceil(len_b / n_b) rounded up to whole 32-position blocks, so every
-// pair holds about total / (N - B) positions.  r is the smallest count of
-// rounds whose split length stays within cap_tok; N is lowered when the
-// splits would fall below the minimum split length.  Pairs are enumerated
-// sequence-major: consecutive pairs -- which the dispatcher sends to
-// different XCDs -- are different splits.  Every workgroup derives the same
-// plan from the lengths on the device.
+// ------------------------------------------------------------ stream plan
+// The context of sequence b is cut into nblk_b = ceil(len_b / 32) blocks of
+// 32 positions.  The blocks of all sequences, in sequence order, form one
+// list of TB blocks, cut into N pairs of Q or Q + 1 consecutive blocks (the
+// first R = TB mod N pairs take Q + 1), so every pair -- one wave per unit
+// (kv head, block of 16 query heads) -- carries the same work whatever the
+// lengths; a CU's time is the bytes of the waves it holds, so equal pairs
+// keep every CU busy to the end.  N is one round of resident waves
+// (T_pairs), fewer when the pairs would hold less than
+// MK_ATTN_MIN_SPLIT_BLOCKS blocks, more when they would exceed cap_blk (the
+// blocks whose pages one wave can address).  A pair that crosses a sequence
+// boundary works on one segment per sequence it touches.  A segment that
+// covers its whole sequence writes the output; any other writes a partial
+// (m, l, O) to slot pair + b -- unique, and consecutive over the pairs of one
+// sequence -- which the merge kernel combines (LSE merge,
+// ops/attention_ops.py:534-550).  Every wave derives the same plan from the
+// lengths on the device.
 __device__ __forceinline__ int clamp_len(int len, int max_s) {
   return len < 0 ? 0 : (len > max_s ? max_s : len);
 }
+
+__device__ __forceinline__ int nblk_of(int len) { return (len + kBlockPos - 1) / kBlockPos; }
 
 __device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
 #pragma unroll
@@ -274,69 +282,92 @@ __device__ __forceinline__ int64_t wave_incl_scan_i64(int64_t v, int lane) {
   return v;
 }
 
-struct PairPlan {
-  int b;       // sequence (-1: past the last pair)
-  int s;       // split of b (>= nsplit: an idle pair)
-  int st;      // positions per split of b
-  int nsplit;  // splits of b actually used
-  int first;   // first pair of b
-  int len;     // positions of b
+struct StreamPlan {
+  int64_t TB;  // blocks over all sequences
+  int64_t N;   // pairs in use (0 when every sequence is empty)
+  int64_t Q;   // blocks per pair; the first R pairs take one more
+  int64_t R;
+  int len0;    // lane b < 64: positions of sequence b
+  int start0;  // lane b < 64: global index of sequence b's first block
 };
 
-__device__ __forceinline__ int64_t pairs_before(int64_t extra, int64_t cum, int64_t total) {
-  return total > 0 ? (extra * cum) / total : 0;
+__device__ __forceinline__ int64_t pair_start(const StreamPlan& sp, int64_t p) {
+  return p * sp.Q + (p < sp.R ? p : sp.R);
 }
 
-// by_seq false: the plan of pair `key`; true: the plan of sequence `key`
-// (its first pair, split length and split count; s = 0).
-__device__ PairPlan plan_pairs(const PagedArgs& a, int key, bool by_seq, int lane) {
+// pair holding global block g (g < TB)
+__device__ __forceinline__ int64_t pair_of(const StreamPlan& sp, int64_t g) {
+  const int64_t big = sp.R * (sp.Q + 1);
+  return g < big ? g / (sp.Q + 1) : sp.R + (g - big) / sp.Q;
+}
+
+__device__ StreamPlan stream_plan(const PagedArgs& a, int lane) {
   const int max_s = a.MB << a.lgP;
-  const int64_t B = a.B, T = a.T_pairs;
-  // total length
-  int64_t total = 0;
-  for (int c = 0; c < a.B; c += 64) {
+  StreamPlan sp;
+  sp.len0 = lane < a.B ? clamp_len(a.lengths[lane], max_s) : 0;
+  const int nb0 = nblk_of(sp.len0);
+  int64_t tb = nb0;
+  for (int c = 64; c < a.B; c += 64) {
     const int b = c + lane;
-    total += b < a.B ? clamp_len(a.lengths[b], max_s) : 0;
+    tb += b < a.B ? nblk_of(clamp_len(a.lengths[b], max_s)) : 0;
   }
-  total = wave_sum_i64(total);
-  // pair count N
-  const int64_t cap_blk = a.cap_tok / kBlockPos;
-  int64_t r = B / T + 1;
-  if (r < MK_ATTN_ROUNDS) r = MK_ATTN_ROUNDS;
-  while ((total + (r * T - B) * kBlockPos - 1) / ((r * T - B) * kBlockPos) > cap_blk) ++r;
-  int64_t N = r * T;
-  const int64_t min_st = (int64_t)(MK_ATTN_MIN_SPLIT_BLOCKS < cap_blk ? MK_ATTN_MIN_SPLIT_BLOCKS : cap_blk) *
-                         kBlockPos;
-  if ((N - B) * min_st > total) N = B + (total + min_st - 1) / min_st;
-  if (N <= B) N = B + 1;
-  const int64_t extra = N - B;
-  // locate the pair: P_b (pairs up to and including b) = b + 1 + floor(extra cum_b / total)
-  PairPlan pl;
-  pl.b = -1;
+  sp.TB = wave_sum_i64(tb);
+  sp.start0 = (int)(wave_incl_scan_i64(nb0, lane) - nb0);
+  int64_t N = a.T_pairs;
+  const int64_t minb = MK_ATTN_MIN_SPLIT_BLOCKS < a.cap_blk ? MK_ATTN_MIN_SPLIT_BLOCKS : a.cap_blk;
+  if (sp.TB < N * minb) N = (sp.TB + minb - 1) / minb;
+  if (N > 0 && (sp.TB + N - 1) / N > a.cap_blk) N = (sp.TB + a.cap_blk - 1) / a.cap_blk;
+  if (N > sp.TB) N = sp.TB;
+  sp.N = N;
+  sp.Q = N > 0 ? sp.TB / N : 0;
+  sp.R = N > 0 ? sp.TB - sp.Q * N : 0;
+  return sp;
+}
+
+// Length and first global block of sequence b (wave-uniform b < B).
+__device__ void seq_info(const PagedArgs& a, const StreamPlan& sp, int b, int lane, int* len,
+                         int64_t* start) {
+  if (b < 64) {
+    *len = __builtin_amdgcn_readlane(sp.len0, b);
+    *start = __builtin_amdgcn_readlane(sp.start0, b);
+    return;
+  }
+  const int max_s = a.MB << a.lgP;
+  int64_t carry = wave_sum_i64(nblk_of(sp.len0));
+  for (int c = 64; c < a.B; c += 64) {
+    const int bb = c + lane;
+    const int l = bb < a.B ? clamp_len(a.lengths[bb], max_s) : 0;
+    const int64_t incl = wave_incl_scan_i64(nblk_of(l), lane) + carry;
+    if (b < c + 64) {
+      *len = __shfl(l, b - c, 64);
+      *start = __shfl(incl, b - c, 64) - nblk_of(*len);
+      return;
+    }
+    carry = __shfl(incl, 63, 64);
+  }
+  *len = 0;
+  *start = carry;
+}
+
+// The sequence holding global block g (g < TB) and its first global block.
+__device__ int seq_of_block(const PagedArgs& a, const StreamPlan& sp, int64_t g, int lane, int64_t* start) {
+  const int max_s = a.MB << a.lgP;
   int64_t carry = 0;
   for (int c = 0; c < a.B; c += 64) {
-    const int b = c + lane;
-    const int len = b < a.B ? clamp_len(a.lengths[b], max_s) : 0;
-    const int64_t cum = wave_incl_scan_i64(len, lane) + carry;
-    const int64_t P_incl = (int64_t)b + 1 + pairs_before(extra, cum, total);
-    const int64_t P_excl = (int64_t)b + pairs_before(extra, cum - len, total);
-    const uint64_t before = __ballot(b < a.B && P_incl <= key);
-    const int k = by_seq ? key - c : __popcll(before);
-    if (k >= 0 && k < 64 && c + k < a.B) {
-      pl.b = c + k;
-      pl.first = (int)__shfl(P_excl, k, 64);
-      pl.len = __shfl(len, k, 64);
-      const int n_b = (int)(__shfl(P_incl, k, 64) - pl.first);
-      pl.s = by_seq ? 0 : key - pl.first;
-      int st = (pl.len + n_b - 1) / n_b;
-      st = (st + kBlockPos - 1) / kBlockPos * kBlockPos;
-      pl.st = st < kBlockPos ? kBlockPos : st;
-      pl.nsplit = pl.len > 0 ? (pl.len + pl.st - 1) / pl.st : 1;
-      return pl;
+    const int bb = c + lane;
+    const int nb = c == 0 ? nblk_of(sp.len0) : (bb < a.B ? nblk_of(clamp_len(a.lengths[bb], max_s)) : 0);
+    const int64_t incl = wave_incl_scan_i64(nb, lane) + carry;
+    // sequences ending at or before g come first (ends never decrease)
+    const uint64_t before = __ballot(bb < a.B && incl <= g);
+    const int k = __popcll(before);
+    if (k < 64 && c + k < a.B) {
+      *start = __shfl(incl, k, 64) - __shfl(nb, k, 64);
+      return c + k;
     }
-    carry = __shfl(cum, 63, 64);
+    carry = __shfl(incl, 63, 64);
   }
-  return pl;
+  *start = carry;
+  return a.B - 1;
 }
 
 // Merge the split partials of query heads [h0, h0 + hcount) of sequence b
@@ -350,6 +381,67 @@ __device__ void merge_heads(const PagedArgs& a, int b, int h0, int hcount, int f
     const int h = h0 + hh;
     const float* ml = a.ws_ml + ((size_t)first * a.Hq + h) * 2;
     const float* po = a.ws + ((size_t)first * a.Hq + h) * D + lane * DPT;
+    if (nsplit <= 64) {
+      // one round trip: lane s holds split s's (m, l); the O partials go out
+      // in batches of 32 that do not wait for (m, l).  Indices past the last
+      // split re-read it and get weight exp2(-inf) = 0.
+      constexpr int BATCH = 32;
+      const f32x2 v = lane < nsplit ? *reinterpret_cast<const f32x2*>(ml + (size_t)lane * sstride * 2)
+                                    : (f32x2){-INFINITY, 0.0f};
+      float acc[DPT];
+#pragma unroll
+      for (int e = 0; e < DPT; ++e) acc[e] = 0.0f;
+      float x[BATCH][DPT];
+#pragma unroll
+      for (int k = 0; k < BATCH; ++k) {
+        const float* p = po + (size_t)(k < nsplit ? k : nsplit - 1) * sstride * D;
+        if constexpr (DPT == 2) {
+          const f32x2 y = *reinterpret_cast<const f32x2*>(p);
+          x[k][0] = y[0];
+          x[k][1] = y[1];
+        } else {
+          x[k][0] = p[0];
+        }
+      }
+      const float M = wave_max(v[0]);
+      const float Mu = M == -INFINITY ? 0.0f : M;
+      const float w = __builtin_amdgcn_exp2f(v[0] - Mu);
+      const float L = wave_sum(v[1] * w);
+#pragma unroll
+      for (int k = 0; k < BATCH; ++k) {
+        const float wk = __shfl(w, k, 64);
+#pragma unroll
+        for (int e = 0; e < DPT; ++e) acc[e] += wk * x[k][e];
+      }
+      if (nsplit > BATCH) {  // wave-uniform
+#pragma unroll
+        for (int k = 0; k < BATCH; ++k) {
+          const int sk = BATCH + k;
+          const float* p = po + (size_t)(sk < nsplit ? sk : nsplit - 1) * sstride * D;
+          if constexpr (DPT == 2) {
+            const f32x2 y = *reinterpret_cast<const f32x2*>(p);
+            x[k][0] = y[0];
+            x[k][1] = y[1];
+          } else {
+            x[k][0] = p[0];
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < BATCH; ++k) {
+          const float wk = __shfl(w, BATCH + k, 64);
+#pragma unroll
+          for (int e = 0; e < DPT; ++e) acc[e] += wk * x[k][e];
+        }
+      }
+      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+      AT* op = reinterpret_cast<AT*>(a.out) + ((size_t)b * a.Hq + h) * D + lane * DPT;
+      if constexpr (DPT == 2) {
+        *reinterpret_cast<uint32_t*>(op) = pack_act2<AT>(acc[0] * inv, acc[1] * inv);
+      } else {
+        op[0] = from_f32<AT>(acc[0] * inv);
+      }
+      continue;
+    }
     float M = -INFINITY;
     for (int s0 = 0; s0 < nsplit; s0 += 64) {
       const int s = s0 + lane;
@@ -406,36 +498,48 @@ __device__ void merge_heads(const PagedArgs& a, int b, int h0, int hcount, int f
   }
 }
 
-// One wave per (sequence, query head): merges the head's split partials
-// (sequences finished in one split were written by the attention kernel).
+// One wave per (sequence, query head): merges the partials of the pairs the
+// sequence spans (a sequence inside one pair was written by the attention
+// kernel) and writes zeros for a sequence with no position.
 template <typename AT, int D>
 __global__ __launch_bounds__(64) void paged_attn_merge_kernel(const PagedArgs a) {
   const int lane = threadIdx.x;
   const int b = (int)blockIdx.x / a.Hq;
   const int h = (int)blockIdx.x - b * a.Hq;
-  const PairPlan pl = plan_pairs(a, b, true, lane);
-  if (pl.nsplit <= 1) return;
-  merge_heads<AT, D>(a, b, h, 1, pl.first, pl.nsplit, lane);
+  const StreamPlan sp = stream_plan(a, lane);
+  int len;
+  int64_t start;
+  seq_info(a, sp, b, lane, &len, &start);
+  if (len == 0) {
+    AT* op = reinterpret_cast<AT*>(a.out) + ((size_t)b * a.Hq + h) * D;
+    for (int d = lane; d < D; d += 64) op[d] = from_f32<AT>(0.0f);
+    return;
+  }
+  const int64_t p0 = pair_of(sp, start), p1 = pair_of(sp, start + nblk_of(len) - 1);
+  if (p0 == p1) return;
+  merge_heads<AT, D>(a, b, h, 1, (int)(p0 + b), (int)(p1 - p0 + 1), lane);
 }
 
-// Where one split's positions live.  Two addressing modes:
+// Where one segment's positions live.  The page ids of all segments of a
+// pair sit in one list, segment by segment (a segment's first page at index
+// po).  Two addressing modes:
 //  * PT (page size a multiple of 16): a 16-position tile never crosses a
 //    page, so each tile needs one page id -- read from a register that holds
-//    the split's page ids (lane i: page i, at most 64) -- and the tile's row
-//    base is wave-uniform; lanes add fixed offsets.
-//  * otherwise: every position looks its page up in an LDS copy of the
-//    split's block-table row.
+//    the list (lane i: entry i, at most 64) -- and the tile's row base is
+//    wave-uniform; lanes add fixed offsets.
+//  * otherwise: every position looks its page up in an LDS copy of the list.
 struct SplitCtx {
-  const int* spage;  // !PT: LDS page ids of the split (invalid as -1)
-  int my_page;       // PT: page id of logical block blk0 + lane (invalid as -1)
-  int blk0;          // first logical block of the split
+  const int* spage;  // !PT: LDS page list (invalid as -1)
+  int my_page;       // PT: page list entry `lane` (invalid as -1)
+  int blk0;          // logical page of the segment's first position
+  int po;            // list index of that page
   int t_begin, t_end, lgP, Pm, Hkv, hkv;
   // !PT: row index (page, slot, kv head) of position t, clamped into the
-  // split; *ok says whether t is a real, mapped position
+  // segment; *ok says whether t is a real, mapped position
   __device__ __forceinline__ uint32_t row(int t, bool* ok) const {
     const bool in = t < t_end;
     const int tc = in ? t : t_end - 1;
-    const int pg = spage[(tc >> lgP) - blk0];
+    const int pg = spage[po + (tc >> lgP) - blk0];
     *ok = in && pg >= 0;
     const uint32_t p = pg < 0 ? 0u : (uint32_t)pg;
     return (((p << lgP) + (uint32_t)(tc & Pm)) * (uint32_t)Hkv) + (uint32_t)hkv;
@@ -445,7 +549,7 @@ struct SplitCtx {
   __device__ __forceinline__ uint32_t tile_row(int tu, uint32_t* bits) const {
     const int last = (t_end - 1) & ~15;
     const int tc = tu < last ? tu : last;
-    const int pg = __builtin_amdgcn_readlane(my_page, (tc >> lgP) - blk0);
+    const int pg = __builtin_amdgcn_readlane(my_page, po + (tc >> lgP) - blk0);
     int n = t_end - tu;
     n = n < 0 ? 0 : (n > 16 ? 16 : n);
     *bits = pg < 0 ? 0u : (n == 16 ? 0xFFFFu : ((1u << n) - 1u));
@@ -454,15 +558,20 @@ struct SplitCtx {
   }
 };
 
-// Lane-constant byte offsets of the PT addressing mode.
+// Lane-constant byte offsets of the PT addressing mode.  The K run r of row
+// r16 sits at k0 + r * KRUN_STRIDE and the V chunk of row 4kb + i at
+// v0 + i * rs (rs, the bytes between positions of a page, is wave-uniform and
+// goes into the scalar base), so two offsets stay live across the block loop.
 template <int KVF, int D, bool SB>
 struct LaneOffsets {
   using F = Fmt<KVF, D>;
   static constexpr int NKS = KVF == 0 ? 0 : (SB ? F::NRUN : F::KSTEPS);
-  uint32_t k[F::NRUN];            // K codes of run r of row r16
-  uint32_t v[4];                  // V chunk of row 4kb + i
+  static constexpr uint32_t KRUN_STRIDE = 32 * F::KRUN * F::BITS / 8;  // dbase(j + KRUN) - dbase(j), bytes
+  uint32_t k0;                     // K codes of run 0 of row r16
+  uint32_t v0;                     // V chunk of row 4kb
+  uint32_t rs;                     // bytes between positions of a page (wave-uniform)
   uint32_t ks[NKS > 0 ? NKS : 1];  // K scale (elements) of the lane's chunks
-  uint32_t vs[4];                 // V scale (elements)
+  uint32_t vs[4];                  // V scale (elements)
 };
 
 template <typename AT, int D, int KVF, bool SB, bool PT>
@@ -485,15 +594,15 @@ __device__ __forceinline__ void load_block(KVBlock<KVF, D, SB>& blk, const Paged
 #pragma unroll
       for (int r = 0; r < F::NRUN; ++r) {
         if constexpr (F::KBYTES_RUN == 16) {
-          blk.k[u][r] = kv_ld128(kt + lo.k[r]);
+          blk.k[u][r] = kv_ld128(kt + lo.k0 + r * LaneOffsets<KVF, D, SB>::KRUN_STRIDE);
         } else {
-          const u32x2 x = kv_ld64(kt + lo.k[r]);
+          const u32x2 x = kv_ld64(kt + lo.k0 + r * LaneOffsets<KVF, D, SB>::KRUN_STRIDE);
           blk.k[u][r] = (u32x4){x[0], x[1], 0u, 0u};
         }
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint8_t* vr = vt + lo.v[i];
+        const uint8_t* vr = (vt + (uint64_t)i * lo.rs) + lo.v0;
         u32x4 x;
         if constexpr (F::VBYTES == 16) {
           x = kv_ld128(vr);
@@ -599,13 +708,126 @@ __device__ __forceinline__ u32x4 v_chunk(const KVBlock<KVF, D, SB>& blk, int p) 
   }
 }
 
+// Segment s of the list, as wave-uniform (scalar) values.
+__device__ __forceinline__ SegDesc seg_at(const SegDesc* sd, int s) {
+  const SegDesc d = sd[s];
+  return SegDesc{__builtin_amdgcn_readfirstlane(d.b), __builtin_amdgcn_readfirstlane(d.t0),
+                 __builtin_amdgcn_readfirstlane(d.t1), __builtin_amdgcn_readfirstlane(d.po)};
+}
+
+// Page-list entry i of a pair: the page of logical block
+// (t0_s >> lgP) + (i - po_s) of sequence b_s, s the last segment with
+// po_s <= i; -1 for an id outside [0, NP).
+__device__ __forceinline__ int page_entry(const PagedArgs& a, int i, int nseg, const SegDesc* sd) {
+  int b = 0, pg = 0;
+  for (int s = 0; s < nseg; ++s) {
+    const SegDesc d = seg_at(sd, s);
+    const int po = d.po & ((1 << 30) - 1);
+    if (i >= po) {
+      b = d.b;
+      pg = (d.t0 >> a.lgP) + (i - po);
+    }
+  }
+  const int p = a.bt[(size_t)b * a.MB + pg];
+  return (p >= 0 && p < a.NP) ? p : -1;
+}
+
+// Point the addressing context at a segment.
+__device__ __forceinline__ void set_segment(SplitCtx& c, const SegDesc d) {
+  c.t_begin = d.t0;
+  c.t_end = d.t1;
+  c.po = d.po & ((1 << 30) - 1);
+  c.blk0 = c.t_begin >> c.lgP;
+}
+
+// Dynamic LDS bytes per wave: the staged q operands of segments
+// 1 .. kQSlots-1, then the segment list.
+template <int D>
+__host__ __device__ constexpr size_t attn_wave_lds() {
+  return (size_t)(kQSlots - 1) * (D / 32) * 64 * 16 + kMaxSegs * sizeof(SegDesc);
+}
+
+// q^T operand of sequence b: lane (head r16, kb) gets q[b, h0 + r16][dbase(j, kb) .. +8]
+// (zeros for heads past hcount), in the K dequant order.
+template <typename AT, int D, int KVF>
+__device__ __forceinline__ void load_q(const PagedArgs& a, int b, int h0, int hcount, int r16, int kb,
+                                       u32x4* qv) {
+  using F = Fmt<KVF, D>;
+  const bool hv = r16 < hcount;
+  const AT* qp = reinterpret_cast<const AT*>(a.q) + ((size_t)b * a.Hq + h0 + (hv ? r16 : 0)) * D;
+#pragma unroll
+  for (int j = 0; j < F::KSTEPS; ++j) {
+    const u32x4 x = ldg128(qp + F::dbase(j, kb));
+    qv[j] = hv ? qperm<KVF>(x) : (u32x4){0u, 0u, 0u, 0u};
+  }
+}
+
+// q of segment s >= 1: from its LDS slot, or (past kQSlots) from global memory.
+template <typename AT, int D, int KVF>
+__device__ __forceinline__ void begin_segment(const PagedArgs& a, u32x4* qv, const u32x4* qslots, int s,
+                                              const SegDesc* sd, int h0, int hcount, int lane, int r16, int kb) {
+  constexpr int KSTEPS = Fmt<KVF, D>::KSTEPS;
+  if (s < kQSlots) {
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) qv[j] = qslots[((s - 1) * KSTEPS + j) * 64 + lane];
+  } else {
+    load_q<AT, D, KVF>(a, seg_at(sd, s).b, h0, hcount, r16, kb, qv);
+  }
+}
+
+// Write segment s's result: the output when the segment is its whole
+// sequence, else the partial (O unnormalised, m, l) in slot pair + b.
+// Lane holds O[head 4kb + i][d = r16*DPL + vslot(j)].
+template <typename AT, int D, int KVF>
+__device__ __forceinline__ void write_segment(const PagedArgs& a, const f32x4* o, float m_run, float l_run,
+                                              const SegDesc d, int pair, int h0, int hcount) {
+  using F = Fmt<KVF, D>;
+  constexpr int DPL = F::DPL;
+  // lane-derived values are recomputed here so they need not stay live
+  // across the block loop
+  const int lane = (int)__lane_id();
+  const int r16 = lane & 15, kb = lane >> 4;
+  const int b = d.b;
+  const bool whole = (d.po >> 30) & 1;
+  float lv[4], mv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lv[i] = __shfl(l_run, 4 * kb + i, 64);
+    mv[i] = __shfl(m_run, 4 * kb + i, 64);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int h = 4 * kb + i;
+    if (h >= hcount) continue;
+    float nat[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) nat[F::vslot(j)] = o[j][i];
+    if (whole) {
+      const float inv = lv[i] > 0.0f ? 1.0f / lv[i] : 0.0f;
+      uint32_t w[DPL / 2];
+#pragma unroll
+      for (int e = 0; e < DPL / 2; ++e) w[e] = pack_act2<AT>(nat[2 * e] * inv, nat[2 * e + 1] * inv);
+      AT* op = reinterpret_cast<AT*>(a.out) + ((size_t)b * a.Hq + h0 + h) * D + r16 * DPL;
+      if constexpr (DPL == 8) *reinterpret_cast<u32x4*>(op) = (u32x4){w[0], w[1], w[2], w[3]};
+      else *reinterpret_cast<u32x2*>(op) = (u32x2){w[0], w[1]};
+    } else {
+      const size_t slot = (size_t)(pair + b) * a.Hq + h0 + h;
+      float* po = a.ws + slot * D + r16 * DPL;
+#pragma unroll
+      for (int e = 0; e < DPL / 4; ++e)
+        reinterpret_cast<f32x4*>(po)[e] = (f32x4){nat[4 * e], nat[4 * e + 1], nat[4 * e + 2], nat[4 * e + 3]};
+      if (r16 == 0) *reinterpret_cast<f32x2*>(a.ws_ml + slot * 2) = (f32x2){mv[i], lv[i]};
+    }
+  }
+}
+
 // Softmax scores are kept in base 2.  The running max of a head is only
 // raised when a block's max exceeds it by more than kLazyMax (so p <= 2^8,
 // exact in fp16/bf16 exponent range); the O rescale runs only then.
 constexpr float kLazyMax = 8.0f;
 
 template <typename AT, int D, int KVF, bool SB, bool PT>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void paged_attn_kernel(
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void paged_attn_kernel(
     const PagedArgs a) {
   using F = Fmt<KVF, D>;
   using Blk = KVBlock<KVF, D, SB>;
@@ -615,56 +837,88 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
   const int lane = threadIdx.x & 63;
   const int r16 = lane & 15;
   const int kb = lane >> 4;
-  // workgroup -> (pair, unit group); wave -> (kv head, block of 16 query heads)
-  // one wave per (pair, unit): consecutive waves are the units of one pair
-  const int pair = (int)blockIdx.x / a.units;
-  const int unit = (int)blockIdx.x - pair * a.units;
+  // workgroup -> (pair, group of wg_units units); wave -> unit = (kv head,
+  // block of 16 query heads).  The units of a pair read the same pages (one
+  // kv head's slice of every position each), so they share a workgroup: the
+  // CU then streams whole pages instead of every XCD fetching a strided
+  // slice of the same page.
+  // With one unit per workgroup the dispatcher's round-robin over XCDs
+  // would give each XCD one kv head; rotating the units by the pair index
+  // spreads every head over all XCDs.
+  const int groups = a.units / a.wg_units;
+  const int pair = (int)blockIdx.x / groups;
+  const int unit = (((int)blockIdx.x - pair * groups) * a.wg_units + (int)(threadIdx.x >> 6) +
+                    (a.wg_units == 1 ? pair : 0)) % a.units;
   const int hkv = unit / a.HB;
   const int hb = unit - hkv * a.HB;
-  const PairPlan pl = plan_pairs(a, pair, false, lane);
-  // past the last pair, or a pair the rounding of its sequence's split
-  // length left empty
-  if (pl.b < 0 || pl.s >= pl.nsplit) return;
-  const int b = pl.b, s = pl.s, nsplit = pl.nsplit;
-  const int t_begin = s * pl.st;
-  const int t_end = min(pl.len, t_begin + pl.st);
+  const StreamPlan sp = stream_plan(a, lane);
+  if (pair >= sp.N) return;  // workgroup-uniform: a pair the plan leaves unused
+  const int64_t g0 = pair_start(sp, pair), g1 = pair_start(sp, pair + 1);
   const int h0 = hkv * a.G + hb * 16;
   const int hcount = min(16, a.G - hb * 16);
+
+  // ---- the pair's segments, in this wave's LDS after its staged q operands
+  // (segments 1 .. kQSlots-1): kMaxSegs descriptors (a pair holds at most
+  // cap_blk <= 64 blocks, so at most 64 segments)
+  extern __shared__ __align__(16) uint8_t attn_dyn[];
+  u32x4* qslots = reinterpret_cast<u32x4*>(attn_dyn + (size_t)(threadIdx.x >> 6) * attn_wave_lds<D>());
+  SegDesc* sd = reinterpret_cast<SegDesc*>(qslots + (kQSlots - 1) * KSTEPS * 64);
+  int nseg = 0, npg = 0;
+  {
+    int64_t st;
+    int b = seq_of_block(a, sp, g0, lane, &st);
+    for (int64_t g = g0; g < g1 && b < a.B; ++b) {
+      int len;
+      seq_info(a, sp, b, lane, &len, &st);
+      const int nb = nblk_of(len);
+      if (nb == 0) continue;
+      const int lbb = (int)(g - st);
+      const int lbe = (int)((int64_t)nb < g1 - st ? (int64_t)nb : g1 - st);
+      const int t0 = lbb * kBlockPos;
+      const int t1 = min(lbe * kBlockPos, len);
+      if (lane == 0) sd[nseg] = SegDesc{b, t0, t1, npg | ((lbb == 0 && lbe == nb) ? (1 << 30) : 0)};
+      npg += ((t1 - 1) >> a.lgP) - (t0 >> a.lgP) + 1;
+      ++nseg;
+      g = st + lbe;
+    }
+  }
+
+  // q^T operands: segment 0's into registers; segments 1 .. kQSlots-1 into
+  // this wave's LDS slots.  They are requested before the page list, so
+  // their latency overlaps the block-table reads the first K/V loads wait on.
+  // Lane (head r16, kb) holds q[h0 + r16][dbase(j, kb) .. +8] for step j.
+  u32x4 qv[KSTEPS];
+  u32x4 qx[kQSlots > 1 ? kQSlots - 1 : 1][KSTEPS];
+  load_q<AT, D, KVF>(a, seg_at(sd, 0).b, h0, hcount, r16, kb, qv);
+#pragma unroll
+  for (int s = 1; s < kQSlots; ++s)
+    load_q<AT, D, KVF>(a, seg_at(sd, s < nseg ? s : 0).b, h0, hcount, r16, kb, qx[s - 1]);
 
   __shared__ int spage[PT ? 1 : kMaxSplitPages];
   SplitCtx c;
   c.spage = spage;
   c.my_page = -1;
-  c.t_begin = t_begin;
-  c.t_end = t_end;
   c.lgP = a.lgP;
   c.Pm = (1 << a.lgP) - 1;
   c.Hkv = a.Hkv;
   c.hkv = hkv;
-  c.blk0 = t_begin >> a.lgP;
-  const int npg = t_end > t_begin ? ((t_end - 1) >> a.lgP) - c.blk0 + 1 : 0;
-  const int32_t* btrow = a.bt + (size_t)b * a.MB + c.blk0;
+  // the host keeps a pair within 64 (PT) / kMaxSplitPages page-list entries
   if constexpr (PT) {
-    // the host keeps a split within 64 pages in this mode
-    if (lane < npg) {
-      const int p = btrow[lane];
-      c.my_page = (p >= 0 && p < a.NP) ? p : -1;
-    }
+    if (lane < npg) c.my_page = page_entry(a, lane, nseg, sd);
   } else {
-    for (int i = threadIdx.x; i < npg; i += blockDim.x) {
-      const int p = btrow[i];
-      spage[i] = (p >= 0 && p < a.NP) ? p : -1;
-    }
+    for (int i = threadIdx.x; i < npg; i += blockDim.x) spage[i] = page_entry(a, i, nseg, sd);
   }
 
+#pragma unroll
+  for (int s = 1; s < kQSlots; ++s)
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) qslots[((s - 1) * KSTEPS + j) * 64 + lane] = qx[s - 1][j];
   LaneOffsets<KVF, D, SB> lo;
   if constexpr (PT) {
     const uint32_t rs = (uint32_t)a.Hkv * F::ROW_BYTES;  // bytes between positions of a page
-#pragma unroll
-    for (int r = 0; r < F::NRUN; ++r)
-      lo.k[r] = (uint32_t)r16 * rs + (uint32_t)(F::dbase(r * F::KRUN, kb) * F::BITS / 8);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lo.v[i] = (uint32_t)(4 * kb + i) * rs + (uint32_t)(r16 * F::VBYTES);
+    lo.rs = rs;
+    lo.k0 = (uint32_t)r16 * rs + (uint32_t)(F::dbase(0, kb) * F::BITS / 8);
+    lo.v0 = (uint32_t)(4 * kb) * rs + (uint32_t)(r16 * F::VBYTES);
     if constexpr (KVF != 0) {
       const uint32_t ss = (uint32_t)a.Hkv * a.ngroups;  // scale elements between positions
 #pragma unroll
@@ -677,17 +931,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
     }
   }
 
-  // q^T operand: lane (head r16, kb) holds q[h0 + r16][dbase(j, kb) .. +8] for step j
-  u32x4 qv[KSTEPS];
-  {
-    const bool hv = r16 < hcount;
-    const AT* qp = reinterpret_cast<const AT*>(a.q) + ((size_t)b * a.Hq + h0 + (hv ? r16 : 0)) * D;
-#pragma unroll
-    for (int j = 0; j < KSTEPS; ++j) {
-      const u32x4 x = ldg128(qp + F::dbase(j, kb));
-      qv[j] = hv ? qperm<KVF>(x) : (u32x4){0u, 0u, 0u, 0u};
-    }
-  }
   if constexpr (!PT) __syncthreads();
 
   float m_run = -INFINITY;  // per head r16 (replicated over kb)
@@ -784,11 +1027,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
     }
   };
 
-  // Blocks 2k and 2k+1 stream through buffers A and B.  Each buffer has one
-  // load site, so its registers are the same on every trip; B starts empty
-  // (mask 0: consuming it changes nothing) and a block index past the end is
-  // clamped to the last block and masked off.
-  const int nblk = (t_end - t_begin + kBlockPos - 1) / kBlockPos;  // 0 for an empty sequence
+  // Blocks 2k and 2k+1 of the pair stream through buffers A and B.  Each
+  // buffer has one load site, so its registers are the same on every trip; B
+  // starts empty (mask 0: consuming it changes nothing) and a block index past
+  // the end reloads the last block, masked off.  Loads run one block ahead of
+  // the consumes and cross segment boundaries: the load side (c, segL) and the
+  // consume side (segC) each step to the next segment when they reach it.
+  const int nbt = (int)(g1 - g0);
   Blk A, Bq;
 #pragma unroll
   for (int u = 0; u < 2; ++u)
@@ -805,53 +1050,62 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
     for (int q = 0; q < 8; ++q) Bq.vs[q] = 0u;
   }
   Bq.mask = 0u;
-  for (int i = 0; i < nblk; i += 2) {
-    load_block<AT, D, KVF, SB, PT>(A, a, c, lo, t_begin + kBlockPos * i, r16, kb);
+
+  int segL = 0, jL0 = 0, jL1 = 0;  // load side: segment, its first and end pair-local block
+  set_segment(c, seg_at(sd, 0));
+  jL1 = nblk_of(c.t_end - c.t_begin);
+  int segC = 0, jC1 = jL1;         // consume side: segment and its end block
+
+  for (int i = 0; i < nbt; i += 2) {
+    if (i >= jL1) {  // wave-uniform
+      ++segL;
+      jL0 = jL1;
+      set_segment(c, seg_at(sd, segL));
+      jL1 = jL0 + nblk_of(c.t_end - c.t_begin);
+    }
+    load_block<AT, D, KVF, SB, PT>(A, a, c, lo, c.t_begin + kBlockPos * (i - jL0), r16, kb);
     __builtin_amdgcn_sched_barrier(0);
     consume(Bq);  // block i-1 (empty on the first trip)
-    const bool has1 = i + 1 < nblk;
-    load_block<AT, D, KVF, SB, PT>(Bq, a, c, lo, t_begin + kBlockPos * (has1 ? i + 1 : i), r16, kb);
+    const bool has1 = i + 1 < nbt;
+    if (has1 && i + 1 >= jL1) {  // wave-uniform
+      ++segL;
+      jL0 = jL1;
+      set_segment(c, seg_at(sd, segL));
+      jL1 = jL0 + nblk_of(c.t_end - c.t_begin);
+    }
+    load_block<AT, D, KVF, SB, PT>(Bq, a, c, lo, c.t_begin + kBlockPos * ((has1 ? i + 1 : i) - jL0), r16, kb);
     if (!has1) Bq.mask = 0u;
     __builtin_amdgcn_sched_barrier(0);
-    consume(A);
-  }
-  consume(Bq);  // the last odd block (or an empty one)
-
-  // ---- write: lane holds O[head 4kb + i][d = r16*DPL + vslot(j)]
-  float lv[4], mv[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    lv[i] = __shfl(l_run, 4 * kb + i, 64);
-    mv[i] = __shfl(m_run, 4 * kb + i, 64);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int h = 4 * kb + i;
-    if (h >= hcount) continue;
-    const size_t bh = (size_t)b * a.Hq + h0 + h;
-    float nat[DPL];
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) nat[F::vslot(j)] = o[j][i];
-    if (nsplit == 1) {
-      const float inv = lv[i] > 0.0f ? 1.0f / lv[i] : 0.0f;
-      uint32_t w[DPL / 2];
-#pragma unroll
-      for (int e = 0; e < DPL / 2; ++e) w[e] = pack_act2<AT>(nat[2 * e] * inv, nat[2 * e + 1] * inv);
-      AT* op = reinterpret_cast<AT*>(a.out) + bh * D + r16 * DPL;
-      if constexpr (DPL == 8) *reinterpret_cast<u32x4*>(op) = (u32x4){w[0], w[1], w[2], w[3]};
-      else *reinterpret_cast<u32x2*>(op) = (u32x2){w[0], w[1]};
-    } else {
-      const size_t slot = (size_t)(pl.first + s) * a.Hq + (bh - (size_t)b * a.Hq);
-      float* po = a.ws + slot * D + r16 * DPL;
-#pragma unroll
-      for (int e = 0; e < DPL / 4; ++e)
-        reinterpret_cast<f32x4*>(po)[e] = (f32x4){nat[4 * e], nat[4 * e + 1], nat[4 * e + 2], nat[4 * e + 3]};
-      if (r16 == 0) {
-        float* pml = a.ws_ml + slot * 2;
-        *reinterpret_cast<f32x2*>(pml) = (f32x2){mv[i], lv[i]};
+    if (i >= jC1) {  // wave-uniform: block i opens the next segment
+      write_segment<AT, D, KVF>(a, o, m_run, l_run, seg_at(sd, segC), pair, h0, hcount);
+      ++segC;
+      {
+        const SegDesc d = seg_at(sd, segC);
+        jC1 += nblk_of(d.t1 - d.t0);
       }
+      begin_segment<AT, D, KVF>(a, qv, qslots, segC, sd, h0, hcount, lane, r16, kb);
+      m_run = -INFINITY;
+      l_run = 0.0f;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) o[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+    consume(A);
+    if (has1 && i + 1 >= jC1) {  // wave-uniform: block i + 1 (consumed next trip) opens the next segment
+      write_segment<AT, D, KVF>(a, o, m_run, l_run, seg_at(sd, segC), pair, h0, hcount);
+      ++segC;
+      {
+        const SegDesc d = seg_at(sd, segC);
+        jC1 += nblk_of(d.t1 - d.t0);
+      }
+      begin_segment<AT, D, KVF>(a, qv, qslots, segC, sd, h0, hcount, lane, r16, kb);
+      m_run = -INFINITY;
+      l_run = 0.0f;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) o[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
     }
   }
+  consume(Bq);  // the last odd block (or an empty one)
+  write_segment<AT, D, KVF>(a, o, m_run, l_run, seg_at(sd, segC), pair, h0, hcount);
 }
 
 // --------------------------------------------------------------- generic path
@@ -966,34 +1220,49 @@ inline bool fast_ok(int64_t D, int kvf, int dtype, int64_t gs, int64_t P, int64_
   return true;
 }
 
-// Host half of the split plan: workgroup shape, pairs aimed for (one per
-// resident workgroup slot: two waves per SIMD, four SIMDs per CU), the
-// longest split, and the pair count bound the workspace is sized for.
+// Host half of the stream plan: workgroup shape, pairs per round (one per
+// resident wave slot: two waves per SIMD, four SIMDs per CU), the most
+// blocks one pair may hold, and the pair count bound.
 inline void split_plan(PagedArgs& a) {
   a.units = a.Hkv * a.HB;
-  // resident waves per round: two per SIMD, four SIMDs per CU
-  int64_t T = (int64_t)device_cus() * 8 / a.units;
+  const int64_t cus = device_cus();
+  int64_t T = cus * 8 / a.units;
   if (T < 1) T = 1;
   a.T_pairs = (int)T;
-  // pages one split may touch: 64 (one per lane) when tiles sit inside
-  // pages, else the LDS table's size
-  const int64_t max_pages = (a.P % 16 == 0) ? 64 : kMaxSplitPages;
-  int64_t cap = ((max_pages - 1) * a.P) / kBlockPos * kBlockPos;
-  if (cap < kBlockPos) cap = kBlockPos;
-  a.cap_tok = (int)cap;
-  // The device plan uses N <= r T pairs with r the smallest count of rounds,
-  // at least max(B/T + 1, MK_ATTN_ROUNDS), whose split fits the cap: either
-  // r is that floor (r T <= B + T or MK_ATTN_ROUNDS T) or the split at r - 1
-  // exceeded the cap, (r-1) T - B < total / cap, so r T < B max_ctx / cap + B + T.
-  const int64_t max_ctx = (int64_t)a.MB * a.P;
-  const int64_t by_cap = ((int64_t)a.B * max_ctx + cap - 1) / cap;
-  // (the minimum-split lowering only shrinks N; an all-empty batch uses B + 1)
-  a.max_pairs = (int)(T + by_cap + a.B + (int64_t)MK_ATTN_ROUNDS * T);
+  // Segments start at 32-position block boundaries, so a pair of n blocks
+  // touches at most 2n pages for P >= 16 (32/P pages per block below): its
+  // page list must fit 64 lanes (P % 16 == 0) or the LDS table, and its
+  // segments the 64 lanes that describe them.
+  int64_t cap;
+  if (a.P % 16 == 0) cap = 32;
+  else cap = (int64_t)kMaxSplitPages * a.P / kBlockPos;
+  if (cap > 64) cap = 64;
+  if (cap < 1) cap = 1;
+  a.cap_blk = (int)cap;
+  const int64_t blk_per_seq = ((int64_t)a.MB * a.P + kBlockPos - 1) / kBlockPos;
+  const int64_t by_cap = ((int64_t)a.B * blk_per_seq + cap - 1) / cap;
+  a.max_pairs = (int)(T > by_cap ? T : by_cap);
+  // The units of a pair share a workgroup (up to 8 waves, one CU) when the
+  // block table allows enough pairs for a workgroup per CU; with fewer pairs
+  // (short total context) one-wave workgroups spread them over all CUs.
+  const int64_t minb = MK_ATTN_MIN_SPLIT_BLOCKS < cap ? MK_ATTN_MIN_SPLIT_BLOCKS : cap;
+  int64_t pairs = (a.B * blk_per_seq + minb - 1) / minb;
+  if (pairs > T) pairs = T;
+  int wg = 1;
+  for (int d = 8; d >= 1; --d)
+    if (a.units % d == 0) {
+      wg = d;
+      break;
+    }
+  a.wg_units = pairs * (a.units / wg) >= cus ? wg : 1;
 }
 
-// Workspace: [O partials, max_pairs * Hq * D fp32][(m, l), max_pairs * Hq * 2 fp32]
+// Partial slots: pair + sequence < max_pairs + B.
+inline int64_t workspace_slots(const PagedArgs& a) { return (int64_t)a.max_pairs + a.B; }
+
+// Workspace: [O partials, slots * Hq * D fp32][(m, l), slots * Hq * 2 fp32]
 inline size_t workspace_need(const PagedArgs& a, int64_t D) {
-  return (size_t)a.max_pairs * a.Hq * (D + 2) * sizeof(float);
+  return (size_t)workspace_slots(a) * a.Hq * (D + 2) * sizeof(float);
 }
 
 int attention_launch(PagedArgs a, int64_t D, int kvf, int dtype, size_t ws_bytes,
@@ -1005,13 +1274,14 @@ int attention_launch(PagedArgs a, int64_t D, int kvf, int dtype, size_t ws_bytes
     split_plan(a);
     const size_t need = workspace_need(a, D);
     if (!a.ws || ws_bytes < need || !mk_aligned(a.ws, 16)) return MK_ERR_INVALID;
-      a.ws_ml = a.ws + (size_t)a.max_pairs * a.Hq * D;
-    const dim3 grid((unsigned)((int64_t)a.max_pairs * a.units));
-    const dim3 block(64u);
-#define MK_PA2(AT, DD, KF, SB)                                                        \
-  do {                                                                               \
-    if (a.P % 16 == 0) paged_attn_kernel<AT, DD, KF, SB, true><<<grid, block, 0, st>>>(a); \
-    else paged_attn_kernel<AT, DD, KF, SB, false><<<grid, block, 0, st>>>(a);       \
+    a.ws_ml = a.ws + (size_t)workspace_slots(a) * a.Hq * D;
+    const dim3 grid((unsigned)((int64_t)a.max_pairs * (a.units / a.wg_units)));
+    const dim3 block(64u * (unsigned)a.wg_units);
+    const size_t qlds = (size_t)a.wg_units * (D == 128 ? attn_wave_lds<128>() : attn_wave_lds<64>());
+#define MK_PA2(AT, DD, KF, SB)                                                               \
+  do {                                                                                      \
+    if (a.P % 16 == 0) paged_attn_kernel<AT, DD, KF, SB, true><<<grid, block, qlds, st>>>(a); \
+    else paged_attn_kernel<AT, DD, KF, SB, false><<<grid, block, qlds, st>>>(a);            \
   } while (0)
 #define MK_PA(AT, DD, KF, SB) MK_PA2(AT, DD, KF, SB)
     if (kvf == 0) {

@@ -63,12 +63,12 @@ def attention(q, K, V, lengths, valid, scale):
         keep = np.nonzero(valid[b, :n])[0]
         if keep.size == 0:
             continue
-        for h in range(Hq):
-            k = K[b, keep, h // g].astype(np.float64)
-            v = V[b, keep, h // g].astype(np.float64)
-            s = k @ q[b, h].astype(np.float64) * scale
-            p = np.exp(s - s.max())
-            out[b, h] = (p / p.sum()) @ v
+        for kh in range(Hkv):  # the g query heads of kv head kh together
+            k = K[b, keep, kh].astype(np.float64)
+            v = V[b, keep, kh].astype(np.float64)
+            s = (q[b, kh * g:(kh + 1) * g].astype(np.float64) @ k.T) * scale
+            p = np.exp(s - s.max(axis=1, keepdims=True))
+            out[b, kh * g:(kh + 1) * g] = (p / p.sum(axis=1, keepdims=True)) @ v
     return out
 
 

@@ -111,6 +111,39 @@ def test_paged_gqa_attention(dev, B, Hq, Hkv, D, P, mb, dtype):
                  what=f"B{B} Hq{Hq} Hkv{Hkv} D{D} P{P}")
 
 
+@pytest.mark.parametrize("P", [16, 8])
+def test_paged_attention_many_short_sequences(dev, P):
+    """Pairs of the stream plan that cross many sequences: 70 sequences
+    (two 64-lane chunks), most of them a block or less, empty ones between,
+    so a pair spans more sequences than the q operands staged per wave."""
+    B, Hq, Hkv, D = 70, 8, 2, 128
+    mb = 128 // P  # 128 positions per sequence at most
+    pattern = [0, 1, 5, 31, 32, 33, 0, 2, 64, 17, 0, 0, 3, 100]
+    lengths = [pattern[i % len(pattern)] for i in range(B)]
+    lengths[5] = mb * P  # one full-length sequence
+    q, Kp, Vp, bt, lengths = _case(77 + P, B, Hq, Hkv, D, P, mb, lengths=lengths)
+    qt, Kt, Vt = (_t(a, dev, torch.float16) for a in (q, Kp, Vp))
+    got = gqa.paged_gqa_decode_attention(qt[:, None], Kt, Vt, to_dev(bt, dev), to_dev(lengths, dev))[:, 0]
+    ref = op.paged_attention(qt.float().cpu().numpy(), Kt.float().cpu().numpy(), Vt.float().cpu().numpy(), bt,
+                             lengths)
+    assert_close(got, ref, rtol=1e-2, atol=1e-3, what=f"short sequences P{P}")
+    assert torch.all(got[lengths == 0] == 0)
+
+
+def test_paged_attention_pairs_at_block_cap(dev):
+    """A context long enough that equal pairs would exceed the blocks one wave
+    can address: the plan adds pairs beyond one round of resident waves."""
+    # MQA with 256 query heads: 16 waves per pair, so one round holds few pairs
+    B, Hq, Hkv, D, P = 2, 256, 1, 64, 16
+    mb = 10000  # 160000 positions per sequence
+    q, Kp, Vp, bt, lengths = _case(91, B, Hq, Hkv, D, P, mb, lengths=[mb * P, mb * P - 77])
+    qt, Kt, Vt = (_t(a, dev, torch.float16) for a in (q, Kp, Vp))
+    got = gqa.paged_gqa_decode_attention(qt[:, None], Kt, Vt, to_dev(bt, dev), to_dev(lengths, dev))[:, 0]
+    ref = op.paged_attention(qt.float().cpu().numpy(), Kt.float().cpu().numpy(), Vt.float().cpu().numpy(), bt,
+                             lengths)
+    assert_close(got, ref, rtol=1e-2, atol=1e-3, what="long context")
+
+
 def test_paged_attention_edge_lengths(dev):
     q, Kp, Vp, bt, _ = _case(5, 4, 8, 2, 128, 16, 70)
     lengths = np.array([0, 1, 17, 70 * 16], np.int32)
