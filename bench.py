@@ -3,8 +3,8 @@
 Timed workload (the configuration the metric is quoted on):
 one q4 quantized-MLP decode step at Llama-3-8B shapes -- hidden 4096,
 intermediate 14336, group 64, fp16 scales and zero points, batch M=1:
-    residual add + RMSNorm      (mk_residual_rms_norm)
-    gate/up q4 matvec + SwiGLU  (mk_q4_gate_up, 2 x 14336x4096)
+    residual add + RMSNorm + gate/up q4 matvec + SwiGLU
+                                (mk_q4_rmsnorm_gate_up, 2 x 14336x4096, one kernel)
     down q4 matvec + residual   (mk_q4_matvec, 4096x14336)
 Each step uses the next of several distinct weight sets (>= 512 MB in total)
 so the 256 MB Infinity Cache cannot serve the weights.  The steps are
@@ -14,8 +14,8 @@ launch overhead is not in the timed region.
 value = algorithmic HBM bytes of the step (packed codes + fp16 scales/zeros +
 activations in/out) / measured step time, in GB/s.  The JSON line also
 carries:
-  roofline      -- the dominant kernel (q4 gate/up) timed alone with HIP
-                   events, against the 8 TB/s HBM peak;
+  roofline      -- the dominant kernel (norm + q4 gate/up) timed alone with
+                   HIP events, against the 8 TB/s HBM peak;
   cpu_baseline  -- the numpy oracle (the reference's array path restated)
                    timed on this host for a bounded sample of the same step;
   extra         -- M=4/8 and q8 variants, and paged GQA decode attention at
@@ -36,9 +36,9 @@ sys.path.insert(0, os.path.join(ROOT, "mlx-metal-kernels_amd"))
 
 PEAK_GBS = 8000.0
 HIDDEN, INTER, GROUP = 4096, 14336, 64
-DOMINANT_KERNEL = "gemv_dot_kernel<4, 2, 2>"  # q4 gate/up + SwiGLU at M = 1
+DOMINANT_KERNEL = "gemv_dot_kernel<4, 2, 2, true>"  # residual + RMSNorm + q4 gate/up + SwiGLU, M = 1
 COPY_KERNEL_HINT = "copy"                      # torch's device-to-device copy kernel
-TRAFFIC_SUMMARY = "gemv_dot_q4_gate_up_M1_traffic.json"
+TRAFFIC_SUMMARY = "gemv_dot_q4_rmsnorm_gate_up_M1_traffic.json"
 
 
 def _parse():
@@ -93,13 +93,15 @@ def make_mlp_set(dev, bits, seed):
 
 
 def mlp_bytes(M, bits):
-    """Algorithmic HBM bytes of one MLP step (matches the launches above)."""
+    """Algorithmic HBM bytes of one MLP step: front = residual add + RMSNorm +
+    gate/up + SwiGLU (codes, scales, zero points; x, residual, norm weight
+    read; z, normed, mlp written), down = down projection + residual (codes,
+    scales, zero points; mlp and z read, out written)."""
     G_h, G_i = HIDDEN // GROUP, INTER // GROUP
     code = bits / 8
-    gate_up = 2 * (INTER * HIDDEN * code + INTER * G_h * 4) + M * HIDDEN * 2 + M * INTER * 2
+    front = 2 * (INTER * HIDDEN * code + INTER * G_h * 4) + 3 * M * HIDDEN * 2 + 2 * M * HIDDEN * 2 + M * INTER * 2
     down = HIDDEN * INTER * code + HIDDEN * G_i * 4 + M * INTER * 2 + 2 * M * HIDDEN * 2
-    prologue = 5 * M * HIDDEN * 2
-    return int(gate_up), int(down), int(prologue)
+    return int(front), int(down)
 
 
 # ----------------------------------------------------------------- timing helpers
@@ -159,7 +161,6 @@ def time_steps(fns, steps, warmup):
 def mlp_step_fns(sets, M, bits, dev):
     import torch
 
-    import mk.norm_ops as norm
     import mk.quant_ops as qo
 
     x = torch.randn((M, 1, HIDDEN), device=dev).to(torch.float16)
@@ -171,15 +172,14 @@ def mlp_step_fns(sets, M, bits, dev):
         (gw, gs, gz), (uw, us, uz), (dw, ds, dz) = ws
 
         def step():
-            z, n = norm.residual_rms_norm(x, res, nw)
-            mlp = qo.q_gate_up_swiglu(n, gw, uw, gs, us, gz, uz, bits=bits, group_size=GROUP)
+            z, _, mlp = qo.q_rmsnorm_gate_up_swiglu(x, res, nw, gw, uw, gs, us, gz, uz, bits=bits, group_size=GROUP)
             _, out = qo.q_matvec_residual(mlp, dw, ds, dz, z, bits=bits, group_size=GROUP)
             outs["out"] = out
 
-        def gate_up_only():
-            qo.q_gate_up_swiglu(x, gw, uw, gs, us, gz, uz, bits=bits, group_size=GROUP)
+        def front():
+            qo.q_rmsnorm_gate_up_swiglu(x, res, nw, gw, uw, gs, us, gz, uz, bits=bits, group_size=GROUP)
 
-        return step, gate_up_only
+        return step, front
 
     return [make(ws) for ws in sets], (x, res, nw)
 
@@ -278,7 +278,7 @@ def summarize_counters(fetch_csv, write_csv, out_path, copy_mb):
     WRITE_SIZE (KiB per dispatch), each scaled by what the same counter reads
     for the plain copy of ``copy_mb`` MiB run by --calib-copy-mb."""
     copy_bytes = copy_mb * (1 << 20)
-    out = {"kernel": DOMINANT_KERNEL, "workload": "config2 gate/up 2x14336x4096 q4 g64 M=1",
+    out = {"kernel": DOMINANT_KERNEL, "workload": "config2 residual+RMSNorm+gate/up 2x14336x4096 q4 g64 M=1",
            "algorithmic_bytes": None, "copy_bytes": copy_bytes}
     for name, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
         rows = _counter_rows(path, name)
@@ -294,9 +294,9 @@ def summarize_counters(fetch_csv, write_csv, out_path, copy_mb):
                      "copy_kib": round(max(cop), 1), "scale": round(factor, 4),
                      "bytes_per_launch": int(per_launch_kib * 1024.0 * factor)}
     out["traffic_bytes_per_launch"] = out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"]
-    b_gu, _, _ = mlp_bytes(1, 4)
-    out["algorithmic_bytes"] = b_gu
-    out["traffic_over_algorithmic"] = round(out["traffic_bytes_per_launch"] / b_gu, 4)
+    b_front, _ = mlp_bytes(1, 4)
+    out["algorithmic_bytes"] = b_front
+    out["traffic_over_algorithmic"] = round(out["traffic_bytes_per_launch"] / b_front, 4)
     with open(out_path, "w") as f:
         json.dump(out, f, indent=2)
     print(json.dumps(out))
@@ -343,13 +343,13 @@ def main():
     fns, x_res_nw = mlp_step_fns(sets, 1, 4, dev)
     # timed region: exactly `steps` MLP steps
     ms = time_steps([step for step, _ in fns], args.steps, args.warmup)
-    b_gu, b_down, b_pro = mlp_bytes(1, 4)
-    step_bytes = b_gu + b_down + b_pro
+    b_front, b_down = mlp_bytes(1, 4)
+    step_bytes = b_front + b_down
     value = step_bytes / (ms * 1e-3) / 1e9
 
     # dominant kernel alone (same stream, HIP events over the timed region)
-    ms_gu = time_steps([gu for _, gu in fns], args.steps, args.warmup)
-    achieved = b_gu / (ms_gu * 1e-3) / 1e9
+    ms_front = time_steps([front for _, front in fns], args.steps, args.warmup)
+    achieved = b_front / (ms_front * 1e-3) / 1e9
 
     extra = {}
     if not args.no_extra:
@@ -400,8 +400,8 @@ def main():
                    "step_bytes": step_bytes, "frac_of_peak": round(value / PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": load_traffic(),
-                     "kernel": "gemv_dot_kernel<4,2,2> q4 gate/up+SwiGLU 2x14336x4096 M=1",
-                     "bytes_per_launch": b_gu, "us_per_launch": round(ms_gu * 1e3, 3)},
+                     "kernel": "gemv_dot_kernel<4,2,2,true> residual+RMSNorm+q4 gate/up+SwiGLU 2x14336x4096 M=1",
+                     "bytes_per_launch": b_front, "us_per_launch": round(ms_front * 1e3, 3)},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -108,6 +108,27 @@ int mk_q8_gate_up(const void* x, const uint8_t* w_gate, const uint8_t* w_up,
                   void* gate_out, void* up_out, void* mlp_out, int64_t M, int64_t N, int64_t K,
                   int64_t group_size, int act_dtype, int scale_dtype, void* stream);
 
+/* The front of quantized_mlp_block -- ops/mlp_block_ops.py:343-356: residual
+ * add z = x + residual (z_out [M,K]), RMSNorm normed = z * rsqrt(mean(z^2) +
+ * eps) * norm_w (normed_out [M,K]), then the gate/up products and SwiGLU as
+ * mk_q4_gate_up / mk_q8_gate_up.  For q4 with an M = 1 fp16 row, K <= 8192,
+ * fp16 norm weights and fp16 scales this is one launch (the norm runs inside
+ * the gate/up kernel) and normed_out may be NULL; otherwise the norm kernel
+ * and the gate/up kernel run in turn through normed_out, which is then
+ * required (MK_ERR_ARG when NULL).
+ * norm_w_dtype: MK_DT_F16/BF16/F32. */
+int mk_q4_rmsnorm_gate_up(const void* x, const void* residual, const void* norm_w, float eps,
+                          const uint8_t* w_gate, const uint8_t* w_up, const void* s_gate, const void* s_up,
+                          const void* z_gate, const void* z_up, void* z_out, void* normed_out, void* gate_out,
+                          void* up_out, void* mlp_out, int64_t M, int64_t N, int64_t K, int64_t group_size,
+                          int act_dtype, int scale_dtype, int norm_w_dtype, void* stream);
+
+int mk_q8_rmsnorm_gate_up(const void* x, const void* residual, const void* norm_w, float eps,
+                          const uint8_t* w_gate, const uint8_t* w_up, const void* s_gate, const void* s_up,
+                          const void* z_gate, const void* z_up, void* z_out, void* normed_out, void* gate_out,
+                          void* up_out, void* mlp_out, int64_t M, int64_t N, int64_t K, int64_t group_size,
+                          int act_dtype, int scale_dtype, int norm_w_dtype, void* stream);
+
 /* ---------------------------------------------------------------- elementwise / norm */
 
 /* swiglu / fused_swiglu -- ops/activation_ops.py:91-153.

@@ -197,7 +197,16 @@ struct GemvArgs {
   int row_bytes;
   int G;
   int lg;                // log2(group size)
-  int kw;                // waves per workgroup (K split)
+  int kw;                // waves per row group (K split)
+  int rg;                // dot kernel: row groups per workgroup
+  // residual + RMSNorm prologue (NORM dot kernels, M = 1): the product is
+  // taken against n = fp16(z * rsqrt(mean(z^2) + eps) * nw), z = fp16(x +
+  // nres); workgroup 0 writes z and (when nout is given) n
+  const void* nres;      // [K]
+  const void* nw;        // [K] fp16
+  void* zout;            // [K]
+  void* nout;            // [K] or null
+  float eps;
 };
 
 // --------------------------------------------------------------------------
@@ -462,7 +471,24 @@ struct DotFrag {
   u32x4 x[4];
 };
 
-template <int BITS, int NMAT, int EPI>
+// Full 64-lane sum, in every lane.
+__device__ __forceinline__ float wave_total(float v) {
+  v = swap_sum<32>(v, v);
+  v = swap_sum<16>(v, v);
+  v += xor_lane<8>(v);
+  v += xor_lane<4>(v);
+  v += xor_lane<2>(v);
+  return v + xor_lane<1>(v);
+}
+
+// Workgroup layout: rg row groups of R rows (per matrix) x kw waves, one
+// 2048-k slice per wave.  The plain kernel has one row group and each wave
+// reads its slice of x straight from memory.  With the norm prologue (NORM)
+// the workgroup loads x, the residual and the norm weight once, 16 bytes per
+// thread, normalises the row into LDS, and every wave reads its slice from
+// there: two row groups share that work, and the activation traffic per
+// code byte is what keeps the prologue cheap.
+template <int BITS, int NMAT, int EPI, bool NORM>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void gemv_dot_kernel(
     const GemvArgs args) {
   constexpr int R = dot_rows<BITS, NMAT>();
@@ -471,8 +497,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int kw = args.kw;
+  const int grp = wave / kw;     // row group of this wave
+  const int ks = wave - grp * kw;  // k slice of this wave
   const int N = args.N, K = args.K, G = args.G;
-  const int n0 = blockIdx.x * R;
+  const int n0 = ((int)blockIdx.x * args.rg + grp) * R;
   const uint32_t magic = in_vgpr(BITS == 4 ? 0x64006400u : 0x64646464u);
   const f16* x = reinterpret_cast<const f16*>(args.x);
 
@@ -482,42 +510,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
 #pragma unroll
     for (int r = 0; r < R; ++r) wrow[t][r] = args.w[t] + (size_t)min(n0 + r, N - 1) * args.row_bytes;
 
-  // unit u = it * 64 * kw + wave * 64 + lane: one 128-bit code load per row
-  // (two for q8) and four for x; a wave's 64 units are contiguous in k
+  // unit u = ks * 64 + lane: one 128-bit code load per row (two for q8) and
+  // four 16-byte x vectors; a wave's 64 units are contiguous in k
   const int U = K / 32;
-  // branch-free: a lane past the last unit re-reads unit 0 (its sums are
-  // dropped), so all loads sit in one block and vmcnt waits stay exact
-  // x goes out before the codes: vmcnt retires in issue order, so the x
-  // operands are ready after the first waits and row (t, r) computes as soon
-  // as its own code load has landed, overlapping the loads still in flight
-  auto load = [&](int u, DotFrag<BITS, NMAT, R>& f) {
-    const int k0 = (u < U ? u : 0) * 32;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) f.x[j] = ldg128(x + k0 + 8 * j);
-#pragma unroll
-    for (int t = 0; t < NMAT; ++t)
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const uint8_t* p = wrow[t][r] + (uint32_t)(k0 * BITS / 8);
-        f.w[t][r][0] = ldg128_stream(p);
-        if constexpr (BITS == 8) f.w[t][r][BITS == 4 ? 0 : 1] = ldg128_stream(p + 16);
-      }
-  };
+  const int ubase = ks * 64;
+
+  // dynamic LDS: [normalised row, K fp16 | NORM][(s, z) stage per wave]
+  extern __shared__ __align__(16) uint8_t dot_lds[];
+  f16* xrow = reinterpret_cast<f16*>(dot_lds);
+  uint8_t* stage = dot_lds + (NORM ? (size_t)K * 2 : 0) + wave * (NSEG * 2 * SEG_STRIDE);
 
   // Scales and zero points: each wave stages, in its own LDS region, the
   // (s, z) of its rows for the groups its 64 units cover -- NSEG runs of gpw
   // fp16 values (gpw <= 64), fetched with 128-bit loads and stored at a fixed
   // stride of 64 entries so a row's run sits at a compile-time offset.  They
-  // are requested first, then x and the codes, then the LDS writes (vmcnt is
-  // in order: the writes wait for the small loads only).  No workgroup barrier
-  // is needed: LDS ops of a wave run in order.
+  // are requested first, then the activations, then the codes (vmcnt retires
+  // in issue order, so each later wait leaves the code loads in flight).
   const int lsv = 8 - args.lg;      // log2(16-byte vectors per run), gpw = 8 << lsv
   const int nvec = NSEG << lsv;     // <= 64 * DOT_SZ_VEC (checked by the dispatcher)
-  extern __shared__ __align__(16) uint8_t dot_stage[];  // kw * NSEG * 128 bytes
-  uint8_t* stage = dot_stage + wave * (NSEG * 2 * SEG_STRIDE);
   u32x4 szv[DOT_SZ_VEC];
   uint32_t sz_zero[DOT_SZ_VEC];
-  const int ubase = wave * 64;
   {
     // branch-free: lanes without a run (or a missing zero tensor) read a valid
     // vector of the same row and drop it, so every load counts in order for
@@ -542,9 +554,43 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
       sz_zero[j] = (uint32_t)isz & (has_z ^ 1u);  // zero tensor absent: z = 0
     }
   }
-  __builtin_amdgcn_sched_barrier(0);  // keep the small loads ahead of the code loads
+  __builtin_amdgcn_sched_barrier(0);  // keep the small loads ahead of the rest
+
+  // activations: NORM -- 16-byte chunks c = threadIdx.x (+ blockDim.x) of x,
+  // the residual and the norm weight, at most two per thread (the dispatcher
+  // keeps K / 8 <= 2 * blockDim.x), clamped so every load issues; otherwise
+  // -- this lane's four vectors of its unit of x.
+  const int nthr = blockDim.x;
+  const int nchunk = K / 8;
+  const bool two = nthr < nchunk;  // workgroup-uniform
+  u32x4 ax[NORM ? 2 : 1], ar[NORM ? 2 : 1], aw[NORM ? 2 : 1];
   DotFrag<BITS, NMAT, R> f;
-  load(ubase + lane, f);
+  const int u = ubase + lane;
+  const int k0 = (u < U ? u : 0) * 32;
+  if constexpr (NORM) {
+    const int c0 = threadIdx.x, c1 = two ? threadIdx.x + nthr : threadIdx.x;
+    const int c1c = c1 < nchunk ? c1 : c0;
+    const f16* rp = reinterpret_cast<const f16*>(args.nres);
+    const f16* wp = reinterpret_cast<const f16*>(args.nw);
+    ax[0] = ldg128(x + 8 * c0);
+    ax[1] = ldg128(x + 8 * c1c);
+    ar[0] = ldg128(rp + 8 * c0);
+    ar[1] = ldg128(rp + 8 * c1c);
+    aw[0] = ldg128(wp + 8 * c0);
+    aw[1] = ldg128(wp + 8 * c1c);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.x[j] = ldg128(x + k0 + 8 * j);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // the activation loads stay ahead of the codes
+#pragma unroll
+  for (int t = 0; t < NMAT; ++t)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint8_t* p = wrow[t][r] + (uint32_t)(k0 * BITS / 8);
+      f.w[t][r][0] = ldg128_stream(p);
+      if constexpr (BITS == 8) f.w[t][r][BITS == 4 ? 0 : 1] = ldg128_stream(p + 16);
+    }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < DOT_SZ_VEC; ++j) {
@@ -555,14 +601,64 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
           sz_zero[j] ? (u32x4){0u, 0u, 0u, 0u} : szv[j];
     }
   }
-  __builtin_amdgcn_wave_barrier();
+
+  if constexpr (NORM) {
+    const int c0 = threadIdx.x, c1 = threadIdx.x + nthr;
+    const bool has0 = c0 < nchunk, has1 = two && c1 < nchunk;
+    {
+      // z = fp16(x + r) and the row's sum of z^2 (the packed fp16 add rounds
+      // the exact sum once, as the norm kernel's fp32 add-then-round does for
+      // fp16 inputs), then n = fp16((z * inv) * w) in fp32 -- the arithmetic
+      // of rms_norm_vec_kernel; workgroup 0 writes z and n out
+      u32x4 zz[2];
+      float ss = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          zz[i][e] = bitcast<uint32_t>(bitcast<f16x2>(ax[i][e]) + bitcast<f16x2>(ar[i][e]));
+          const float sq = dot2(zz[i][e], zz[i][e], 0.0f);
+          ss += (i == 0 ? has0 : has1) ? sq : 0.0f;
+        }
+      ss = wave_total(ss);
+      __shared__ float norm_part[8];
+      if (lane == 0) norm_part[wave] = ss;
+      __syncthreads();
+      float tot = 0.0f;
+      for (int w = 0; w < (int)(nthr >> 6); ++w) tot += norm_part[w];
+      const float inv = rsqrtf(tot / (float)K + args.eps);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        if (!(i == 0 ? has0 : has1)) continue;
+        const int c = i == 0 ? c0 : c1;
+        u32x4 nv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const f16x2 zh = bitcast<f16x2>(zz[i][e]);
+          const f16x2 wh = bitcast<f16x2>(aw[i][e]);
+          const f16x2 nh = {(f16)(((float)zh[0] * inv) * (float)wh[0]),
+                            (f16)(((float)zh[1] * inv) * (float)wh[1])};
+          nv[e] = bitcast<uint32_t>(nh);
+        }
+        *reinterpret_cast<u32x4*>(xrow + 8 * c) = nv;
+        if (blockIdx.x == 0) {
+          *reinterpret_cast<u32x4*>(reinterpret_cast<f16*>(args.zout) + 8 * c) = zz[i];
+          if (args.nout) *reinterpret_cast<u32x4*>(reinterpret_cast<f16*>(args.nout) + 8 * c) = nv;
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.x[j] = *reinterpret_cast<const u32x4*>(xrow + k0 + 8 * j);
+  } else {
+    __builtin_amdgcn_wave_barrier();
+  }
 
   float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
 
   {  // one 64-unit slice per wave (the dispatcher guarantees U <= 64 * kw)
-    const int u = ubase + lane;
     // a lane past the last unit computes on x = 0: its codes, offsets and
     // zero-point terms all vanish, so its sums add nothing
     if (u >= U) {
@@ -643,7 +739,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
       }
   }
 
-  // ---- 64-lane reduction (halving butterfly), then across waves in LDS
+  // ---- 64-lane reduction (halving butterfly), then across the row group's
+  // waves in LDS
   reduce_scatter<V, 32>(acc, lane);
   const float tot = acc[0];
   int idx = 0;
@@ -654,11 +751,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
   constexpr int QUAD = 64 / V;  // lanes holding the same index
   if ((lane & (QUAD - 1)) == 0) red[wave][idx] = tot;
   __syncthreads();
-  if (wave != 0 || lane >= R) return;
+  if (ks != 0 || lane >= R) return;
   float v0 = 0.0f, v1 = 0.0f;
   for (int w = 0; w < kw; ++w) {
-    v0 += red[w][lane];
-    if constexpr (NMAT == 2) v1 += red[w][R + lane];
+    v0 += red[wave + w][lane];
+    if constexpr (NMAT == 2) v1 += red[wave + w][R + lane];
   }
   const int nn = n0 + lane;
   if (nn < N) store_out<f16, EPI>(args, (size_t)nn, v0, v1);
@@ -748,12 +845,22 @@ int launch_fast(const GemvArgs& a, int gpc, hipStream_t st) {
   return MK_OK;
 }
 
-template <int BITS, int NMAT, int EPI>
-int launch_dot(const GemvArgs& a, hipStream_t st) {
+// Row groups per dot workgroup: one for the plain kernel (measured: sharing
+// x through LDS costs a barrier that outweighs its L2 savings); two for the
+// norm prologue (four at K <= 2048), which keeps K / 8 <= 2 * blockDim.x for
+// K <= 8192 and halves the activation reads per code byte.
+template <bool NORM>
+inline int dot_row_groups(int kw) { return NORM ? (kw >= 2 ? 2 : 4) : 1; }
+
+template <int BITS, int NMAT, int EPI, bool NORM = false>
+int launch_dot(GemvArgs a, hipStream_t st) {
   constexpr int R = dot_rows<BITS, NMAT>();
-  const dim3 grid((a.N + R - 1) / R);
-  const size_t stage_bytes = (size_t)a.kw * NMAT * R * 2 * (2 * SEG_STRIDE);
-  gemv_dot_kernel<BITS, NMAT, EPI><<<grid, dim3(64 * a.kw), stage_bytes, st>>>(a);
+  a.rg = dot_row_groups<NORM>(a.kw);
+  const int rows = R * a.rg;
+  const dim3 grid((unsigned)((a.N + rows - 1) / rows));
+  const dim3 block((unsigned)(64 * a.kw * a.rg));
+  const size_t stage_bytes = (size_t)a.kw * a.rg * NMAT * R * 2 * (2 * SEG_STRIDE);
+  gemv_dot_kernel<BITS, NMAT, EPI, NORM><<<grid, block, (NORM ? (size_t)a.K * 2 : 0) + stage_bytes, st>>>(a);
   MK_CHECK_LAUNCH();
   return MK_OK;
 }
@@ -777,6 +884,49 @@ inline int choose_kw(int64_t N, int64_t K, int kc) {
   return kw;
 }
 
+// Shape facts every launch needs: fills N, K, G, row_bytes and lg of a;
+// returns the groups per 32-code lane chunk of the MFMA path (0: none) and
+// whether the aligned fast layouts apply.
+template <int BITS, int NMAT>
+int gemv_prepare(GemvArgs& a, int64_t N, int64_t K, int64_t gs, bool* fast) {
+  using F = QFmt<BITS>;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.G = (int)((K + gs - 1) / gs);
+  a.row_bytes = BITS == 4 ? (int)((K + 1) / 2) : (int)K;
+  const int lg = ilog2_exact(gs);
+  int gpc = 0;
+  if (lg >= 0) {
+    if (gs >= F::KL) gpc = 1;
+    else if (gs >= 8 && F::KL / gs <= 4) gpc = (int)(F::KL / gs);
+  }
+  bool f = gpc > 0 && (K % F::KL) == 0 && mk_aligned(a.x, 16);
+  for (int t = 0; t < NMAT; ++t) f = f && mk_aligned(a.w[t], 16);
+  a.lg = lg;
+  *fast = f;
+  return gpc;
+}
+
+// The M = 1 dot kernel: one 64-unit (2048-k) slice per wave, <= 8 waves; the
+// (s, z) runs of a slice must be whole 16-byte vectors and fit the stage.
+template <int BITS, int NMAT>
+bool dot_eligible(const GemvArgs& a, bool fast, int64_t mrows, int act_dt, int sc_dt) {
+  const int lg = a.lg;
+  const int64_t K = a.K;
+  const int64_t gpw = lg >= 0 ? (2048 >> lg) : 0;
+  return fast && mrows == 1 && act_dt == MK_DT_F16 && sc_dt == MK_DT_F16 && lg >= 5 && lg <= 8 &&
+         (K % 32) == 0 && K <= 8 * 2048 && (a.G % 8) == 0 && (gpw % 8) == 0 &&
+         (int64_t)NMAT * dot_rows<BITS, NMAT>() * 2 * (gpw / 8) <= 64 * DOT_SZ_VEC &&
+         mk_aligned(a.s[0], 16) && mk_aligned(a.s[NMAT - 1], 16) &&
+         (a.z[0] == nullptr || (mk_aligned(a.z[0], 16) && mk_aligned(a.z[NMAT - 1], 16)));
+}
+
+// waves per dot-kernel workgroup: one per 64-unit slice
+inline int dot_waves(int64_t K) {
+  int64_t kwd = (K / 32 + 63) / 64;
+  return (int)(kwd < 1 ? 1 : (kwd > 8 ? 8 : kwd));
+}
+
 template <int BITS, int NMAT, int EPI>
 int gemv_dispatch(GemvArgs a, int64_t M, int64_t N, int64_t K, int64_t gs, int act_dt, int sc_dt,
                   hipStream_t st) {
@@ -789,20 +939,8 @@ int gemv_dispatch(GemvArgs a, int64_t M, int64_t N, int64_t K, int64_t gs, int a
   for (int t = 0; t < NMAT; ++t) MK_REQUIRE(a.w[t] && a.s[t]);
   MK_REQUIRE(a.x);
 
-  a.N = (int)N;
-  a.K = (int)K;
-  a.G = (int)((K + gs - 1) / gs);
-  a.row_bytes = BITS == 4 ? (int)((K + 1) / 2) : (int)K;
-
-  const int lg = ilog2_exact(gs);
-  int gpc = 0;
-  if (lg >= 0) {
-    if (gs >= F::KL) gpc = 1;
-    else if (gs >= 8 && F::KL / gs <= 4) gpc = (int)(F::KL / gs);
-  }
-  bool fast = gpc > 0 && (K % F::KL) == 0 && mk_aligned(a.x, 16);
-  for (int t = 0; t < NMAT; ++t) fast = fast && mk_aligned(a.w[t], 16);
-  a.lg = lg;
+  bool fast;
+  const int gpc = gemv_prepare<BITS, NMAT>(a, N, K, gs, &fast);
 
   const int64_t mblocks = (M + 15) / 16;
   const size_t xe = 2;  // activation element size
@@ -817,21 +955,8 @@ int gemv_dispatch(GemvArgs a, int64_t M, int64_t N, int64_t K, int64_t gs, int a
     if (a.y0) b.y0 = (char*)a.y0 + (size_t)m0 * N * xe;
     if (a.y1) b.y1 = (char*)a.y1 + (size_t)m0 * N * xe;
     if (a.y2) b.y2 = (char*)a.y2 + (size_t)m0 * N * xe;
-    // dot kernel: one 64-unit (2048-k) slice per wave, <= 8 waves; the
-    // (s, z) runs of a slice must be whole 16-byte vectors and fit the stage
-    const int64_t gpw = lg >= 0 ? (2048 >> lg) : 0;
-    const bool dot_ok = fast && mrows == 1 && act_dt == MK_DT_F16 && sc_dt == MK_DT_F16 &&
-                        lg >= 5 && lg <= 8 && (K % 32) == 0 && K <= 8 * 2048 &&
-                        (a.G % 8) == 0 && (gpw % 8) == 0 &&
-                        (int64_t)NMAT * dot_rows<BITS, NMAT>() * 2 * (gpw / 8) <= 64 * DOT_SZ_VEC &&
-                        mk_aligned(a.s[0], 16) && mk_aligned(a.s[NMAT - 1], 16) &&
-                        (a.z[0] == nullptr || (mk_aligned(a.z[0], 16) && mk_aligned(a.z[NMAT - 1], 16)));
-    if (dot_ok) {
-      // one 64-unit slice per wave when K allows (K <= 16384), else loop
-      const int64_t units = K / 32;
-      int64_t kwd = (units + 63) / 64;
-      kwd = kwd < 1 ? 1 : (kwd > 8 ? 8 : kwd);
-      b.kw = (int)kwd;
+    if (dot_eligible<BITS, NMAT>(b, fast && mk_aligned(b.x, 16), mrows, act_dt, sc_dt)) {
+      b.kw = dot_waves(K);
       rc = launch_dot<BITS, NMAT, EPI>(b, st);
     } else if (fast) {
       b.kw = choose_kw(N, K, F::KC);
@@ -907,6 +1032,57 @@ int gate_up_entry(const void* x, const uint8_t* wg, const uint8_t* wu, const voi
                                              reinterpret_cast<hipStream_t>(stream));
 }
 
+// Residual add + RMSNorm + gate/up (+ SwiGLU) of one MLP block: one launch
+// (the norm as the dot kernel's prologue) for an M = 1 fp16 q4 decode row the
+// dot kernel takes, else the norm kernel and then the gate/up launch (q8's
+// doubled code registers leave no room for the prologue's operands).
+template <int BITS>
+int norm_gate_up_entry(const void* x, const void* residual, const void* norm_w, float eps, const uint8_t* wg,
+                       const uint8_t* wu, const void* sg, const void* su, const void* zg, const void* zu,
+                       void* z_out, void* normed_out, void* gate_out, void* up_out, void* mlp_out, int64_t M,
+                       int64_t N, int64_t K, int64_t gs, int act_dt, int sc_dt, int nw_dt, void* stream) {
+  MK_REQUIRE(x && residual && norm_w && z_out && wg && wu && sg && su);
+  MK_REQUIRE(gate_out || up_out || mlp_out);
+  MK_REQUIRE(M >= 0 && N > 0 && K > 0 && gs > 0 && N < (1LL << 31) && K < (1LL << 31));
+  MK_REQUIRE(act_dt == MK_DT_F16 || act_dt == MK_DT_BF16);
+  MK_REQUIRE(sc_dt == MK_DT_F16 || sc_dt == MK_DT_F32);
+  MK_REQUIRE(nw_dt == MK_DT_F16 || nw_dt == MK_DT_BF16 || nw_dt == MK_DT_F32);
+  if (M == 0) return MK_OK;
+  GemvArgs a = {};
+  a.x = x;
+  a.w[0] = wg;
+  a.w[1] = wu;
+  a.s[0] = sg;
+  a.s[1] = su;
+  a.z[0] = zg;
+  a.z[1] = zu;
+  a.y0 = gate_out;
+  a.y1 = up_out;
+  a.y2 = mlp_out;
+  bool fast;
+  gemv_prepare<BITS, 2>(a, N, K, gs, &fast);
+  if constexpr (BITS == 4) {
+    // K <= 8192: the row fits two 16-byte chunks per thread of the workgroup
+    if (nw_dt == MK_DT_F16 && K <= 4 * 2048 && dot_eligible<BITS, 2>(a, fast, M, act_dt, sc_dt) &&
+        mk_aligned(residual, 16) &&
+        mk_aligned(norm_w, 16) && mk_aligned(z_out, 16) && (!normed_out || mk_aligned(normed_out, 16))) {
+      a.M = 1;
+      a.kw = dot_waves(K);
+      a.nres = residual;
+      a.nw = norm_w;
+      a.zout = z_out;
+      a.nout = normed_out;
+      a.eps = eps;
+      return launch_dot<BITS, 2, EPI_GATE_UP, true>(a, reinterpret_cast<hipStream_t>(stream));
+    }
+  }
+  MK_REQUIRE(normed_out);  // the two-launch path passes the normalised rows through it
+  const int rc = mk_residual_rms_norm(x, residual, norm_w, z_out, normed_out, M, K, eps, act_dt, nw_dt, stream);
+  if (rc != MK_OK) return rc;
+  return gate_up_entry<BITS>(normed_out, wg, wu, sg, su, zg, zu, gate_out, up_out, mlp_out, M, N, K, gs, act_dt,
+                             sc_dt, stream);
+}
+
 }  // namespace
 
 extern "C" {
@@ -939,6 +1115,26 @@ int mk_q8_gate_up(const void* x, const uint8_t* w_gate, const uint8_t* w_up, con
                   int64_t group_size, int act_dtype, int scale_dtype, void* stream) {
   return gate_up_entry<8>(x, w_gate, w_up, s_gate, s_up, z_gate, z_up, gate_out, up_out, mlp_out,
                           M, N, K, group_size, act_dtype, scale_dtype, stream);
+}
+
+int mk_q4_rmsnorm_gate_up(const void* x, const void* residual, const void* norm_w, float eps,
+                          const uint8_t* w_gate, const uint8_t* w_up, const void* s_gate, const void* s_up,
+                          const void* z_gate, const void* z_up, void* z_out, void* normed_out, void* gate_out,
+                          void* up_out, void* mlp_out, int64_t M, int64_t N, int64_t K, int64_t group_size,
+                          int act_dtype, int scale_dtype, int norm_w_dtype, void* stream) {
+  return norm_gate_up_entry<4>(x, residual, norm_w, eps, w_gate, w_up, s_gate, s_up, z_gate, z_up, z_out,
+                               normed_out, gate_out, up_out, mlp_out, M, N, K, group_size, act_dtype, scale_dtype,
+                               norm_w_dtype, stream);
+}
+
+int mk_q8_rmsnorm_gate_up(const void* x, const void* residual, const void* norm_w, float eps,
+                          const uint8_t* w_gate, const uint8_t* w_up, const void* s_gate, const void* s_up,
+                          const void* z_gate, const void* z_up, void* z_out, void* normed_out, void* gate_out,
+                          void* up_out, void* mlp_out, int64_t M, int64_t N, int64_t K, int64_t group_size,
+                          int act_dtype, int scale_dtype, int norm_w_dtype, void* stream) {
+  return norm_gate_up_entry<8>(x, residual, norm_w, eps, w_gate, w_up, s_gate, s_up, z_gate, z_up, z_out,
+                               normed_out, gate_out, up_out, mlp_out, M, N, K, group_size, act_dtype, scale_dtype,
+                               norm_w_dtype, stream);
 }
 
 }  // extern "C"

@@ -5,11 +5,13 @@ Composition (ops/mlp_block_ops.py:301-364):
     m = silu(g) * u; d = down(m); out = z + d
 with every intermediate rounded to the activation dtype, as in the reference.
 
-When every stage runs on the HIP backend the block is three launches instead
-of six -- the rounding points are unchanged:
-    1. residual add + RMSNorm             (mk_residual_rms_norm)
-    2. gate + up matvec, SwiGLU epilogue  (mk_q{4,8}_gate_up)
-    3. down matvec, residual epilogue     (mk_q{4,8}_matvec with residual)
+When every stage runs on the HIP backend the block is two launches for a q4
+decode row (three otherwise) instead of six -- the rounding points are
+unchanged:
+    1. residual add + RMSNorm, gate + up matvec, SwiGLU epilogue
+       (mk_q{4,8}_rmsnorm_gate_up: one kernel for a q4 fp16 decode row, the
+       norm kernel then the gate/up kernel otherwise)
+    2. down matvec, residual epilogue     (mk_q{4,8}_matvec with residual)
 """
 
 from __future__ import annotations
@@ -18,14 +20,14 @@ import math
 
 from .activation_ops import fused_swiglu, reference_swiglu, swiglu
 from .fused_ops import reference_residual_add, residual_add
-from .norm_ops import reference_rms_norm, residual_rms_norm, rms_norm
+from .norm_ops import reference_rms_norm, rms_norm
 from .quant_ops import (
     q4_gate_up_matvec_tiled,
     q4_matvec_decode,
     q8_gate_up_matvec_tiled,
     q8_matvec_decode,
-    q_gate_up_swiglu,
     q_matvec_residual,
+    q_rmsnorm_gate_up_swiglu,
     reference_q4_matvec_decode,
     reference_q8_matvec_decode,
 )
@@ -192,13 +194,14 @@ def quantized_mlp_block(x, residual, norm_weight, gate_w, gate_scales, up_w, up_
 
     if _all_hip(norm_backend, matvec_backend, activation_backend, residual_backend):
         _validate_bits(bits)
-        z, normed = residual_rms_norm(x, residual, norm_weight, eps=eps)
+        gate = up = None
         if return_intermediates:
-            gate, up, mlp = q_gate_up_swiglu(normed, gate_w, up_w, gate_scales, up_scales, gate_zeros, up_zeros,
-                                             bits=bits, group_size=group_size, return_gate_up=True)
+            z, normed, gate, up, mlp = q_rmsnorm_gate_up_swiglu(
+                x, residual, norm_weight, gate_w, up_w, gate_scales, up_scales, gate_zeros, up_zeros, bits=bits,
+                group_size=group_size, eps=eps, return_gate_up=True)
         else:
-            mlp = q_gate_up_swiglu(normed, gate_w, up_w, gate_scales, up_scales, gate_zeros, up_zeros,
-                                   bits=bits, group_size=group_size)
+            z, normed, mlp = q_rmsnorm_gate_up_swiglu(x, residual, norm_weight, gate_w, up_w, gate_scales, up_scales,
+                                                      gate_zeros, up_zeros, bits=bits, group_size=group_size, eps=eps)
         _validate_quantized_linear_shapes(mlp.reshape(-1, mlp.shape[-1]), down_w, down_scales, down_zeros,
                                           bits=bits, group_size=group_size, name="quantized_linear")
         down, out2d = q_matvec_residual(mlp, down_w, down_scales, down_zeros, z, bits=bits, group_size=group_size,

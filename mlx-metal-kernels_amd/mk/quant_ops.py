@@ -413,6 +413,51 @@ def q8_gate_up_matvec_tiled(x, gate_q, up_q, gate_scales, up_scales, gate_zeros=
     return gate, up
 
 
+def q_rmsnorm_gate_up_swiglu(x, residual, norm_weight, gate_w, up_w, gate_scales, up_scales, gate_zeros=None,
+                             up_zeros=None, *, bits: int = 4, group_size: int = 32, eps: float = 1e-5,
+                             return_gate_up: bool = False):
+    """The front of the MLP block (ops/mlp_block_ops.py:343-356): z = x +
+    residual, normed = rms_norm(z) * norm_weight, then gate/up and the SwiGLU
+    epilogue -- one HIP launch for a q4 decode row (the norm runs inside the
+    gate/up kernel), else the norm and gate/up kernels in turn.  Returns
+    ``(z, normed, mlp)`` or ``(z, normed, gate, up, mlp)``."""
+    if x.shape != residual.shape:
+        raise ValueError(f"x and residual must have identical shapes, got {tuple(x.shape)}, {tuple(residual.shape)}")
+    x2d, original_shape, rows, k_dim = _normalize_hidden_rows_input(x)
+    _validate_matvec_input_dtype(x2d)
+    if tuple(norm_weight.shape) != (k_dim,):
+        raise ValueError(f"norm_weight must have shape {(k_dim,)}, got {tuple(norm_weight.shape)}")
+    _, _, out_dim = _validate_gate_up_shapes(x2d, gate_w, up_w, gate_scales, up_scales, gate_zeros, up_zeros,
+                                             bits=bits, group_size=group_size)
+    x2d = x2d.contiguous()
+    r2d = residual.reshape(rows, k_dim).to(x2d.dtype).contiguous()
+    nw = norm_weight.contiguous()
+    gw, uw = as_u8(gate_w), as_u8(up_w)
+    dev = _lib.require_device(x2d, r2d, nw, gw, uw, gate_scales, up_scales, gate_zeros, up_zeros)
+    all_f16 = all(t is None or t.dtype == torch.float16 for t in (gate_scales, up_scales, gate_zeros, up_zeros))
+    tgt = torch.float16 if all_f16 else torch.float32
+
+    def cvt(t):
+        return None if t is None else t.to(tgt).contiguous()
+
+    sg, su, zg, zu = cvt(gate_scales), cvt(up_scales), cvt(gate_zeros), cvt(up_zeros)
+    z = torch.empty_like(x2d)
+    normed = torch.empty_like(x2d)
+    gate = torch.empty((rows, out_dim), dtype=x2d.dtype, device=dev) if return_gate_up else None
+    up = torch.empty((rows, out_dim), dtype=x2d.dtype, device=dev) if return_gate_up else None
+    mlp = torch.empty((rows, out_dim), dtype=x2d.dtype, device=dev)
+    name = "mk_q4_rmsnorm_gate_up" if bits == 4 else "mk_q8_rmsnorm_gate_up"
+    _lib.launch(name, dev, _lib.ptr(x2d), _lib.ptr(r2d), _lib.ptr(nw), float(eps), _lib.ptr(gw), _lib.ptr(uw),
+                _lib.ptr(sg), _lib.ptr(su), _lib.ptr(zg), _lib.ptr(zu), _lib.ptr(z), _lib.ptr(normed),
+                _lib.ptr(gate), _lib.ptr(up), _lib.ptr(mlp), rows, out_dim, k_dim, group_size,
+                _lib.dtype_code(x2d.dtype), _lib.dtype_code(tgt), _lib.dtype_code(nw.dtype))
+    outs = [z.reshape(x.shape), normed.reshape(x.shape)]
+    if return_gate_up:
+        outs += [_restore_hidden_rows_output(gate, original_shape), _restore_hidden_rows_output(up, original_shape)]
+    outs.append(_restore_hidden_rows_output(mlp, original_shape))
+    return tuple(outs)
+
+
 def q_gate_up_swiglu(x, gate_w, up_w, gate_scales, up_scales, gate_zeros=None, up_zeros=None, *, bits: int = 4,
                      group_size: int = 32, return_gate_up: bool = False):
     """Gate/up projection with the SwiGLU epilogue fused in: silu(gate) * up

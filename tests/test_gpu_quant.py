@@ -149,6 +149,47 @@ def test_gate_up_and_swiglu_epilogue(dev, bits, rows, N, K, g):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("rows,N,K,g,act", [(1, 14336, 4096, 64, "f16"), (1, 300, 3072, 64, "f16"),
+                                            (1, 256, 4096, 32, "f16"), (3, 50, 96, 32, "f16"),
+                                            (1, 64, 512, 64, "bf16")])
+def test_rmsnorm_gate_up(dev, bits, rows, N, K, g, act):
+    """mk_q{4,8}_rmsnorm_gate_up (one launch for a q4 fp16 row, the norm and
+    gate/up kernels otherwise) against the separate norm kernel and the oracle."""
+    import mk.norm_ops as norm
+
+    rng = np.random.default_rng(31 + rows + N + K)
+    _, sg_stored, sg, zg = quant_weight(rng, N, K, g, bits, "sym")
+    _, su_stored, su, zu = quant_weight(rng, N, K, g, bits, "sym")
+    xt, xf = _x(rng, rows, K, act, dev)
+    rt, rf = _x(rng, rows, K, act, dev)
+    nw = torch.from_numpy((1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)).to(ACT[act]).to(dev)
+    args = (to_dev(sg_stored, dev), to_dev(su_stored, dev), to_dev(sg, dev, torch.float16),
+            to_dev(su, dev, torch.float16), to_dev(zg, dev, torch.float16), to_dev(zu, dev, torch.float16))
+    z, normed, gate, up, mlp = qo.q_rmsnorm_gate_up_swiglu(xt, rt, nw, *args, bits=bits, group_size=g, eps=1e-5,
+                                                           return_gate_up=True)
+    z_ref, n_ref = norm.residual_rms_norm(xt[:, None], rt[:, None], nw, eps=1e-5)
+    assert torch.equal(z, z_ref[:, 0])
+    # the one-launch path sums z^2 in another order: the rsqrt can move by an
+    # ulp, so a normalised element may land one fp16/bf16 step away
+    nd = (normed.float() - n_ref[:, 0].float()).abs()
+    step = n_ref[:, 0].float().abs() * (2.0 ** -10 if act == "f16" else 2.0 ** -7) + 1e-7
+    assert torch.all(nd <= step)
+    # gate/up/mlp against the oracle on the kernel's own normalised row
+    mv = oq.q4_matvec if bits == 4 else oq.q8_matvec
+    nf = normed.float().cpu().numpy()
+    rg = mv(nf, sg_stored, sg.astype(np.float16).astype(np.float32), zg, g, act=act)
+    ru = mv(nf, su_stored, su.astype(np.float16).astype(np.float32), zu, g, act=act)
+    tol = 1e-2 if act == "f16" else 2e-2
+    assert_close(gate, rg, rtol=tol, what="gate")
+    assert_close(up, ru, rtol=tol, what="up")
+    assert_close(mlp, oq.swiglu(gate.float().cpu().numpy(), up.float().cpu().numpy(), act=act), rtol=tol,
+                 what="swiglu epilogue")
+    if act == "f16":  # z against the oracle's residual add (bit-exact)
+        zo = oq.residual_add(xf.astype(np.float16), rf.astype(np.float16))
+        assert np.array_equal(z.cpu().numpy(), zo)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("preset", ["tiled", "fused_experimental", "parallel", "metal"])
 @pytest.mark.parametrize("B,S,D,I,g", [(1, 1, 64, 128, 32), (2, 1, 64, 130, 32), (1, 1, 4096, 14336, 64),
                                        (4, 1, 256, 512, 64)])
