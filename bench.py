@@ -119,7 +119,7 @@ def capture(fns):
             fn()  # warm the allocator outside the graph
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):  # the warm-up stream: its cached workspaces carry over
         for fn in fns:
             fn()
     torch.cuda.synchronize()

@@ -144,6 +144,30 @@ def test_paged_attention_pairs_at_block_cap(dev):
     assert_close(got, ref, rtol=1e-2, atol=1e-3, what="long context")
 
 
+def test_paged_attention_graph_replays(dev):
+    """The one-kernel attention captured in a HIP graph: every replay, with
+    eager calls and synchronisations between them, equals the eager result."""
+    q, Kp, Vp, bt, lengths = _case(12, 6, 32, 8, 128, 16, 60, lengths=[960, 17, 500, 0, 959, 333])
+    qt, Kt, Vt = (_t(a, dev, torch.float16) for a in (q, Kp, Vp))
+    btd, lnd = to_dev(bt, dev), to_dev(lengths, dev)
+    run = lambda: gqa.paged_gqa_decode_attention(qt[:, None], Kt, Vt, btd, lnd)
+    st = torch.cuda.Stream(device=qt.device)
+    st.wait_stream(torch.cuda.current_stream(qt.device))
+    with torch.cuda.stream(st):
+        eager = run()
+    torch.cuda.current_stream(qt.device).wait_stream(st)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        captured = run()
+    for i in range(3):
+        captured.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager), f"replay {i}"
+        _ = run().float().sum().item()  # eager work between replays
+
+
 def test_paged_attention_edge_lengths(dev):
     q, Kp, Vp, bt, _ = _case(5, 4, 8, 2, 128, 16, 70)
     lengths = np.array([0, 1, 17, 70 * 16], np.int32)
