@@ -223,6 +223,60 @@ def attention_config3(dev, steps, warmup):
     }
 
 
+def decode_stack_config5(dev, batches=(1, 32), steps=128, ctx=2048):
+    """Llama-3-8B shape (32 layers, hidden 4096, 32/8
+    heads of 128, intermediate 14336), every projection and the head q4 g64
+    (random N(0, 0.02) weights quantized on the device), paged fp16 KV with
+    P=16 pre-filled with N(0, 1) for a 2048-token prompt (prefill is outside
+    the hot path), then ``steps`` greedy decode steps, each one HIP graph
+    replay.  tok/s = B * steps / wall time of the replays."""
+    import torch
+
+    import mk.llama_layer_ops as ll
+    import mk.llama_stack_ops as ls
+
+    cfg = ll.llama3_8b_like()
+    w = ls.create_random_quantized_llama_stack_weights(cfg, bits=4, group_size=GROUP, device=dev, seed=8)
+    cos, sin = ll.build_rope_tables(cfg, device=dev)
+    G_h = cfg.hidden_size // GROUP
+    layer_bytes = sum(n * k // 2 + n * (k // GROUP) * 4 for n, k in (
+        (cfg.qkv_output_dim(), cfg.hidden_size), (cfg.hidden_size, cfg.hidden_size),
+        (cfg.intermediate_size, cfg.hidden_size), (cfg.intermediate_size, cfg.hidden_size),
+        (cfg.hidden_size, cfg.intermediate_size)))
+    head_bytes = cfg.vocab_size * cfg.hidden_size // 2 + cfg.vocab_size * G_h * 4
+    out = {"workload": "config5_llama3_8b_q4g64_paged_fp16_ctx2048", "steps": steps,
+           "weight_bytes_per_step": cfg.num_hidden_layers * layer_bytes + head_bytes}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(9)
+    for B in batches:
+        cache = ls.init_llama_stack_cache(cfg, B, ctx + steps + 2, dtype=torch.float16, page_size=16, device=dev)
+        for K, V, _ in cache.layer_caches:
+            K.normal_(generator=gen)
+            V.normal_(generator=gen)
+        tokens = torch.randint(0, cfg.vocab_size, (B,), generator=gen, device=dev)
+        pos = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+        graph = ls.DecodeGraph(w, cache, cos, sin, cfg, tokens, pos)  # one eager step, then the capture
+        graph.step()
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(steps):
+            graph.step()
+        ev1.record()
+        torch.cuda.synchronize()
+        ms = ev0.elapsed_time(ev1) / steps
+        kv = B * cfg.num_hidden_layers * (ctx + steps // 2) * cfg.num_key_value_heads * cfg.head_dim * 2 * 2
+        step_bytes = out["weight_bytes_per_step"] + kv
+        out[f"batch{B}"] = {"tokens_per_s": B / (ms * 1e-3), "ms_per_step": ms,
+                            "hbm_gbs": step_bytes / (ms * 1e-3) / 1e9,
+                            "frac_of_peak": step_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS}
+        del graph, cache
+        torch.cuda.empty_cache()
+    del w
+    torch.cuda.empty_cache()
+    return out
+
+
 # ----------------------------------------------------------------- CPU baseline
 
 
@@ -369,6 +423,7 @@ def main():
             torch.cuda.empty_cache()
         torch.cuda.empty_cache()
         extra["paged_attention"] = attention_config3(dev, max(50, args.steps // 3), 10)
+        extra["decode_stack"] = decode_stack_config5(dev)
 
     cpu = None
     if not args.no_cpu:

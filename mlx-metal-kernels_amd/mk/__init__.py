@@ -14,11 +14,14 @@ __all__ = [
     "fused_ops",
     "gqa_ops",
     "kv_cache_ops",
+    "llama_layer_ops",
+    "llama_stack_ops",
     "mlp_block_ops",
     "norm_ops",
     "paged_kv_ops",
     "paged_quantized_kv_ops",
     "quantize_weights",
     "quant_ops",
+    "quantized_decode_block_ops",
     "rope_ops",
 ]

@@ -1,0 +1,238 @@
+"""Quantized Llama-like decode layer on a paged KV cache -- the paged path of
+``ops/llama_layer_ops.py`` over torch tensors.
+
+One decode step of one layer (ops/llama_layer_ops.py:234-428):
+    x_norm = rms_norm(x, input_layernorm)                       mk_rms_norm
+    h = x + o_proj(attn(rope(split(qkv_proj(x_norm)))))          paged_quantized_decode_block
+                                                                 (the residual add in the o-proj
+                                                                  matvec's epilogue)
+    out = quantized_mlp_block(h, 0, post_attention_layernorm)    mk_q{4,8}_rmsnorm_gate_up + down
+Every intermediate is rounded to the activation dtype at the reference's
+points.  The reference raises for a paged multi-layer stack
+(ops/llama_stack_ops.py:129-130); this module implements the layer the stack
+composes.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+
+from .mlp_block_ops import quantized_mlp_block, reference_quantized_mlp_block
+from .norm_ops import reference_rms_norm, rms_norm
+from .quantized_decode_block_ops import paged_quantized_decode_block, reference_paged_quantized_decode_block
+
+
+@dataclass
+class LlamaLikeConfig:
+    """models/llama_config.py:11-104."""
+
+    hidden_size: int
+    intermediate_size: int
+    num_attention_heads: int
+    num_key_value_heads: int
+    head_dim: int
+    num_hidden_layers: int
+    max_position_embeddings: int
+    rope_theta: float = 10000.0
+    rms_norm_eps: float = 1e-5
+    vocab_size: int | None = None
+    tie_word_embeddings: bool = False
+    model_type: str = "llama_like"
+
+    def validate(self) -> "LlamaLikeConfig":
+        """models/llama_config.py:26-46."""
+        if self.hidden_size != self.num_attention_heads * self.head_dim:
+            raise ValueError(
+                "hidden_size must equal num_attention_heads * head_dim, "
+                f"got hidden_size={self.hidden_size}, num_attention_heads={self.num_attention_heads}, "
+                f"head_dim={self.head_dim}")
+        if self.num_attention_heads % self.num_key_value_heads != 0:
+            raise ValueError("num_attention_heads must be divisible by num_key_value_heads, "
+                             f"got {self.num_attention_heads}, {self.num_key_value_heads}")
+        if self.intermediate_size <= self.hidden_size:
+            raise ValueError(f"intermediate_size must be greater than hidden_size, got {self.intermediate_size}, "
+                             f"{self.hidden_size}")
+        if self.max_position_embeddings <= 0:
+            raise ValueError("max_position_embeddings must be positive")
+        if self.num_hidden_layers <= 0:
+            raise ValueError("num_hidden_layers must be positive")
+        return self
+
+    def q_output_dim(self) -> int:
+        return self.validate().num_attention_heads * self.head_dim
+
+    def kv_output_dim(self) -> int:
+        return self.validate().num_key_value_heads * self.head_dim
+
+    def qkv_output_dim(self) -> int:
+        return self.q_output_dim() + 2 * self.kv_output_dim()
+
+
+def llama3_8b_like() -> LlamaLikeConfig:
+    """Llama-3-8B decode shape: 32 layers, hidden 4096,
+    32 query / 8 key-value heads of 128, intermediate 14336, RoPE theta
+    500000, vocabulary 128256."""
+    return LlamaLikeConfig(hidden_size=4096, intermediate_size=14336, num_attention_heads=32, num_key_value_heads=8,
+                           head_dim=128, num_hidden_layers=32, max_position_embeddings=8192, rope_theta=500000.0,
+                           rms_norm_eps=1e-5, vocab_size=128256, model_type="llama3_8b_like").validate()
+
+
+def tiny_gqa_debug_config() -> LlamaLikeConfig:
+    """models/llama_config.py:141-152."""
+    return LlamaLikeConfig(hidden_size=64, intermediate_size=128, num_attention_heads=4, num_key_value_heads=2,
+                           head_dim=16, num_hidden_layers=2, max_position_embeddings=64, vocab_size=256,
+                           model_type="llama_like_tiny_gqa_debug").validate()
+
+
+def build_rope_tables(config: LlamaLikeConfig, seq_len: int | None = None, *, device=None):
+    """models/llama_config.py:107-124: (cos, sin) fp32 [seq_len, head_dim / 2]."""
+    config.validate()
+    n = config.max_position_embeddings if seq_len is None else seq_len
+    if n <= 0:
+        raise ValueError(f"seq_len must be positive, got {n}")
+    if config.head_dim % 2 != 0:
+        raise ValueError(f"head_dim must be even for RoPE, got {config.head_dim}")
+    pos = torch.arange(n, dtype=torch.float32, device=device)
+    inv = 1.0 / (float(config.rope_theta) ** (torch.arange(0, config.head_dim, 2, dtype=torch.float32, device=device)
+                                               / float(config.head_dim)))
+    f = pos[:, None] * inv[None, :]
+    return torch.cos(f), torch.sin(f)
+
+
+@dataclass
+class LlamaLayerKernelWeights:
+    """ops/llama_layer_ops.py:88-145 (q4/q8 codes, scales, zeros per projection)."""
+
+    input_layernorm_weight: Any
+    post_attention_layernorm_weight: Any
+    qkv_w: Any
+    qkv_scales: Any | None = None
+    qkv_zeros: Any | None = None
+    o_w: Any | None = None
+    o_scales: Any | None = None
+    o_zeros: Any | None = None
+    gate_w: Any | None = None
+    gate_scales: Any | None = None
+    gate_zeros: Any | None = None
+    up_w: Any | None = None
+    up_scales: Any | None = None
+    up_zeros: Any | None = None
+    down_w: Any | None = None
+    down_scales: Any | None = None
+    down_zeros: Any | None = None
+    bits: int = 4
+    group_size: int = 32
+
+    def validate(self, config: LlamaLikeConfig) -> "LlamaLayerKernelWeights":
+        """ops/llama_layer_ops.py:110-134."""
+        if self.bits not in (4, 8):
+            raise ValueError(f"bits must be 4 or 8, got {self.bits}")
+        if self.group_size <= 0:
+            raise ValueError(f"group_size must be positive, got {self.group_size}")
+        H = config.hidden_size
+        for name in ("input_layernorm_weight", "post_attention_layernorm_weight"):
+            if tuple(getattr(getattr(self, name), "shape", ())) != (H,):
+                raise ValueError(f"{name} must have shape {(H,)}, got {tuple(getattr(self, name).shape)}")
+
+        def cols(k):
+            return (k + 1) // 2 if self.bits == 4 else k
+
+        expected = {"qkv_w": (config.qkv_output_dim(), cols(H)), "o_w": (H, cols(H)),
+                    "gate_w": (config.intermediate_size, cols(H)), "up_w": (config.intermediate_size, cols(H)),
+                    "down_w": (H, cols(config.intermediate_size))}
+        for name, shp in expected.items():
+            got = getattr(self, name)
+            if got is None or tuple(got.shape) != shp:
+                raise ValueError(f"{name} must have shape {shp}, got {None if got is None else tuple(got.shape)}")
+        return self
+
+
+_ZEROS: dict = {}
+
+
+def _zero_residual(h):
+    """A cached zero tensor shaped like h: the MLP block's residual (the
+    layer feeds h as x and 0 as residual, ops/llama_layer_ops.py:360-395),
+    allocated once rather than on every call (and every graph replay)."""
+    key = (tuple(h.shape), h.dtype, h.device)
+    z = _ZEROS.get(key)
+    if z is None:
+        z = torch.zeros(h.shape, dtype=h.dtype, device=h.device)
+        _ZEROS[key] = z
+    return z
+
+
+def _check_decode(x, config: LlamaLikeConfig, cache, cache_layout: str):
+    if x.ndim != 3 or x.shape[1] != 1 or x.shape[2] != config.hidden_size:
+        raise ValueError(f"x must have shape [B,1,{config.hidden_size}], got {tuple(x.shape)}")
+    if cache_layout != "paged":
+        raise ValueError("this build implements the paged cache layout (cache_layout='paged'); "
+                         f"got {cache_layout!r}")
+    if not isinstance(cache, tuple) or len(cache) != 3:
+        raise ValueError("paged cache must be a tuple (K_pages, V_pages, block_table)")
+    return cache
+
+
+def llama_layer_decode_step(x, weights: LlamaLayerKernelWeights, cache, cos, sin, position, config,
+                            *, cache_layout: str = "paged", return_intermediates: bool = False):
+    """ops/llama_layer_ops.py:234-428, paged layout, all stages on HIP.
+    x [B,1,hidden]; cache (K_pages, V_pages, block_table) updated in place;
+    position int or per-sequence [B].  Returns (out, cache) or
+    (out, cache, intermediates)."""
+    config = config.validate()
+    weights.validate(config)
+    K_pages, V_pages, block_table = _check_decode(x, config, cache, cache_layout)
+    x_norm = rms_norm(x, weights.input_layernorm_weight, eps=config.rms_norm_eps)
+    h, K_pages, V_pages, qkv, attn_out = paged_quantized_decode_block(
+        x_norm, weights.qkv_w, weights.qkv_scales, weights.o_w, weights.o_scales, K_pages, V_pages, block_table, cos,
+        sin, position, qkv_zeros=weights.qkv_zeros, out_zeros=weights.o_zeros, bits=weights.bits,
+        group_size=weights.group_size, H=config.num_attention_heads, num_key_value_heads=config.num_key_value_heads,
+        head_dim=config.head_dim, return_intermediates=True, residual=x)
+    res = quantized_mlp_block(h, _zero_residual(h), weights.post_attention_layernorm_weight, weights.gate_w,
+                              weights.gate_scales, weights.up_w, weights.up_scales, weights.down_w, weights.down_scales,
+                              gate_zeros=weights.gate_zeros, up_zeros=weights.up_zeros, down_zeros=weights.down_zeros,
+                              bits=weights.bits, group_size=weights.group_size, eps=config.rms_norm_eps,
+                              backend_preset="fused_experimental", return_intermediates=return_intermediates)
+    cache = (K_pages, V_pages, block_table)
+    if not return_intermediates:
+        return res, cache
+    out, mi = res
+    return out, cache, {"x_norm": x_norm, "qkv": qkv, "attn_out": attn_out, "h": h, "mlp_norm": mi["normed"],
+                        "gate": mi["gate"], "up": mi["up"], "mlp": mi["mlp"], "down": mi["down"]}
+
+
+def reference_llama_layer_decode_step(x, weights: LlamaLayerKernelWeights, cache, cos, sin, position, config,
+                                      *, cache_layout: str = "paged", return_intermediates: bool = False):
+    """ops/llama_layer_ops.py:214-231 (every stage on the torch reference
+    path; the cache is updated functionally, the input cache untouched)."""
+    config = config.validate()
+    weights.validate(config)
+    K_pages, V_pages, block_table = _check_decode(x, config, cache, cache_layout)
+    x_norm = reference_rms_norm(x, weights.input_layernorm_weight, eps=config.rms_norm_eps)
+    attn_proj, K_pages, V_pages, qkv, attn_out = reference_paged_quantized_decode_block(
+        x_norm, weights.qkv_w, weights.qkv_scales, weights.o_w, weights.o_scales, K_pages, V_pages, block_table, cos,
+        sin, position, qkv_zeros=weights.qkv_zeros, out_zeros=weights.o_zeros, bits=weights.bits,
+        group_size=weights.group_size, H=config.num_attention_heads, num_key_value_heads=config.num_key_value_heads,
+        head_dim=config.head_dim, return_intermediates=True)
+    h = (x.float() + attn_proj.float()).to(x.dtype)
+    res = reference_quantized_mlp_block(h, torch.zeros_like(h), weights.post_attention_layernorm_weight, weights.gate_w,
+                                        weights.gate_scales, weights.up_w, weights.up_scales, weights.down_w,
+                                        weights.down_scales, gate_zeros=weights.gate_zeros, up_zeros=weights.up_zeros,
+                                        down_zeros=weights.down_zeros, bits=weights.bits,
+                                        group_size=weights.group_size, eps=config.rms_norm_eps,
+                                        return_intermediates=return_intermediates)
+    cache = (K_pages, V_pages, block_table)
+    if not return_intermediates:
+        return res, cache
+    out, mi = res
+    return out, cache, {"x_norm": x_norm, "qkv": qkv, "attn_out": attn_out, "h": h, "mlp_norm": mi["normed"],
+                        "gate": mi["gate"], "up": mi["up"], "mlp": mi["mlp"], "down": mi["down"]}
+
+
+def kv_pages_for(config: LlamaLikeConfig, B: int, max_seq_len: int, page_size: int = 16):
+    """Pages per layer cache for B sequences of max_seq_len positions."""
+    return B * math.ceil(max_seq_len / page_size)

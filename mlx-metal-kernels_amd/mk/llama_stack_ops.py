@@ -1,0 +1,249 @@
+"""Quantized Llama-like decode stack on paged KV caches -- what
+``ops/llama_stack_ops.py`` runs for ``cache_layout="paged"`` (the reference
+raises NotImplementedError there, ops/llama_stack_ops.py:129-130, 205-206),
+built from the paged layer of ``mk.llama_layer_ops``.
+
+A decode step (ops/llama_stack_ops.py:352-411): every layer in turn, the
+final RMSNorm, then logits = final_hidden . lm_head^T (a q4/q8 matvec when
+the head is quantized, a dense fp32-accumulated product otherwise) and greedy
+sampling (models/sampling.py:120-124).  ``DecodeGraph`` captures one whole
+step -- embedding gather, 32 layers, head, argmax -- in a HIP graph so a
+token costs one graph launch; positions live in a device tensor the step
+advances in place.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+
+from .llama_layer_ops import (
+    LlamaLayerKernelWeights,
+    LlamaLikeConfig,
+    llama_layer_decode_step,
+    reference_llama_layer_decode_step,
+)
+from .norm_ops import reference_rms_norm, rms_norm
+from .quant_ops import q4_matvec_decode, q8_matvec_decode
+from .quantize_weights import QuantizationConfig, quantize_weight_groupwise
+
+
+@dataclass
+class QuantizedHead:
+    """A q4/q8 [vocab, hidden] output projection (codes, scales, zeros)."""
+
+    w: Any
+    scales: Any
+    zeros: Any | None
+    bits: int = 4
+    group_size: int = 32
+
+    @property
+    def shape(self):
+        return (self.scales.shape[0], self.w.shape[1] * (2 if self.bits == 4 else 1))
+
+
+@dataclass
+class LlamaStackWeights:
+    """ops/llama_stack_ops.py:134-169."""
+
+    layers: list
+    final_norm_weight: Any
+    lm_head: Any | None = None
+    embedding: Any | None = None
+
+    def num_layers(self) -> int:
+        return len(self.layers)
+
+    def validate(self, config: LlamaLikeConfig) -> "LlamaStackWeights":
+        config = config.validate()
+        if len(self.layers) != config.num_hidden_layers:
+            raise ValueError(f"layers must have length {config.num_hidden_layers}, got {len(self.layers)}")
+        if tuple(self.final_norm_weight.shape) != (config.hidden_size,):
+            raise ValueError(f"final_norm_weight must have shape {(config.hidden_size,)}, "
+                             f"got {tuple(self.final_norm_weight.shape)}")
+        if self.embedding is not None and self.embedding.shape[1] != config.hidden_size:
+            raise ValueError(f"embedding must have shape [vocab_size,{config.hidden_size}], "
+                             f"got {tuple(self.embedding.shape)}")
+        if self.lm_head is not None and self.lm_head.shape[1] != config.hidden_size:
+            raise ValueError("lm_head must use the documented [vocab_size, hidden_size] convention with hidden size "
+                             f"{config.hidden_size}, got {tuple(self.lm_head.shape)}")
+        for layer in self.layers:
+            layer.validate(config)
+        return self
+
+
+@dataclass
+class LlamaStackCache:
+    """ops/llama_stack_ops.py:171-192 (paged: one (K_pages, V_pages,
+    block_table) per layer)."""
+
+    layer_caches: list
+    cache_layout: str
+    max_seq_len: int
+    page_size: int | None = None
+
+    def num_layers(self) -> int:
+        return len(self.layer_caches)
+
+
+def init_llama_stack_cache(config: LlamaLikeConfig, B: int, max_seq_len: int, *, cache_layout: str = "paged",
+                           dtype=torch.float16, page_size: int = 16, device=None, block_table=None):
+    """ops/llama_stack_ops.py:195-221 for the paged layout: per layer
+    K/V pages [B * ceil(max_seq_len / P), P, Hkv, D] (zeros) sharing one
+    block table [B, ceil(max_seq_len / P)] (identity unless given)."""
+    config = config.validate()
+    if cache_layout != "paged":
+        raise ValueError(f"this build implements the paged cache layout, got {cache_layout!r}")
+    mb = math.ceil(max_seq_len / page_size)
+    if block_table is None:
+        block_table = torch.arange(B * mb, dtype=torch.int32, device=device).reshape(B, mb)
+    npg = int(block_table.max().item()) + 1 if block_table.numel() else 0
+    shape = (max(npg, B * mb), page_size, config.num_key_value_heads, config.head_dim)
+    caches = [(torch.zeros(shape, dtype=dtype, device=device), torch.zeros(shape, dtype=dtype, device=device),
+               block_table) for _ in range(config.num_hidden_layers)]
+    return LlamaStackCache(caches, "paged", max_seq_len, page_size)
+
+
+def embed_token_ids(token_ids, embedding):
+    """ops/llama_stack_ops.py:224-232: token ids [B] or [B,1] -> [B,1,hidden]."""
+    ids = token_ids.reshape(-1, 1) if token_ids.ndim == 1 else token_ids
+    if ids.ndim != 2:
+        raise ValueError(f"token_ids must have shape [B] or [B,1], got {tuple(token_ids.shape)}")
+    out = embedding.index_select(0, ids.reshape(-1).to(torch.int64))
+    return out.reshape(ids.shape[0], ids.shape[1], -1)
+
+
+def logits_from_hidden(hidden, lm_head):
+    """ops/llama_stack_ops.py:235-240: hidden [B,T,H] . lm_head^T -> fp32
+    logits [B,T,vocab].  A ``QuantizedHead`` runs the q4/q8 matvec (outputs
+    in the activation dtype, then widened); a dense head accumulates in fp32."""
+    if hidden.ndim != 3:
+        raise ValueError(f"hidden must have shape [B,1,H] or [B,T,H], got {tuple(hidden.shape)}")
+    B, T, H = hidden.shape
+    if isinstance(lm_head, QuantizedHead):
+        fn = q4_matvec_decode if lm_head.bits == 4 else q8_matvec_decode
+        y = fn(hidden.reshape(B * T, H), lm_head.w, lm_head.scales, lm_head.zeros, group_size=lm_head.group_size)
+        return y.float().reshape(B, T, -1)
+    return (hidden.reshape(B * T, H).float() @ lm_head.float().t()).reshape(B, T, -1)
+
+
+def greedy_sample(logits):
+    """models/sampling.py:120-124: argmax over the vocabulary (first index on
+    ties) -> int64 [B]."""
+    return torch.argmax(logits.reshape(logits.shape[0], -1), dim=-1)
+
+
+def llama_stack_decode_step(x, stack_weights: LlamaStackWeights, stack_cache: LlamaStackCache, cos, sin, position,
+                            config: LlamaLikeConfig, *, return_intermediates: bool = False, reference: bool = False):
+    """ops/llama_stack_ops.py:352-411 on paged caches.  Returns (logits,
+    final_hidden, cache) when the weights carry an lm_head, else
+    (final_hidden, cache); with return_intermediates the per-layer hidden
+    states are appended as a dict."""
+    config = config.validate()
+    step = reference_llama_layer_decode_step if reference else llama_layer_decode_step
+    norm = reference_rms_norm if reference else rms_norm
+    hidden = x
+    layers_out = []
+    new_caches = []
+    for li, lw in enumerate(stack_weights.layers):
+        hidden, cache = step(hidden, lw, stack_cache.layer_caches[li], cos, sin, position, config)
+        new_caches.append(cache)
+        if return_intermediates:
+            layers_out.append(hidden)
+    final_hidden = norm(hidden, stack_weights.final_norm_weight, eps=config.rms_norm_eps)
+    cache = LlamaStackCache(new_caches, "paged", stack_cache.max_seq_len, stack_cache.page_size)
+    inter = {"layers": layers_out, "final_hidden": final_hidden}
+    if stack_weights.lm_head is None:
+        return (final_hidden, cache, inter) if return_intermediates else (final_hidden, cache)
+    logits = logits_from_hidden(final_hidden, stack_weights.lm_head)
+    if return_intermediates:
+        inter["logits"] = logits
+        return logits, final_hidden, cache, inter
+    return logits, final_hidden, cache
+
+
+def _random_linear(out_dim, in_dim, bits, group_size, gen, device, dtype):
+    w = torch.randn((out_dim, in_dim), generator=gen, device=device, dtype=torch.float32).mul_(0.02).to(dtype)
+    qw = quantize_weight_groupwise(w, QuantizationConfig(bits=bits, group_size=group_size))
+    zeros = torch.full(tuple(qw.scales.shape), 8.0 if bits == 4 else 128.0, dtype=qw.scales.dtype, device=device)
+    return qw.packed_weight, qw.scales, zeros
+
+
+def create_random_quantized_llama_stack_weights(config: LlamaLikeConfig, *, vocab_size=None, bits=4, group_size=32,
+                                                dtype=torch.float16, seed=0, device=None, include_embedding=True,
+                                                include_lm_head=True, quantized_lm_head=True):
+    """ops/llama_stack_ops.py:498-555 on the device: every projection drawn
+    N(0, 0.02) and quantized groupwise (symmetric, zero point 8 / 128),
+    norm weights 1, embedding N(0, 1); the head quantized the same way, or
+    dense N(0, 1) fp16 when ``quantized_lm_head`` is False."""
+    config = config.validate()
+    vocab = vocab_size or config.vocab_size or 128
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    H, I = config.hidden_size, config.intermediate_size
+    layers = []
+    for _ in range(config.num_hidden_layers):
+        qkv = _random_linear(config.qkv_output_dim(), H, bits, group_size, gen, device, dtype)
+        o = _random_linear(H, H, bits, group_size, gen, device, dtype)
+        g = _random_linear(I, H, bits, group_size, gen, device, dtype)
+        u = _random_linear(I, H, bits, group_size, gen, device, dtype)
+        d = _random_linear(H, I, bits, group_size, gen, device, dtype)
+        ones = torch.ones(H, dtype=dtype, device=device)
+        layers.append(LlamaLayerKernelWeights(
+            input_layernorm_weight=ones, post_attention_layernorm_weight=ones.clone(),
+            qkv_w=qkv[0], qkv_scales=qkv[1], qkv_zeros=qkv[2], o_w=o[0], o_scales=o[1], o_zeros=o[2],
+            gate_w=g[0], gate_scales=g[1], gate_zeros=g[2], up_w=u[0], up_scales=u[1], up_zeros=u[2],
+            down_w=d[0], down_scales=d[1], down_zeros=d[2], bits=bits, group_size=group_size))
+    final_norm = torch.ones(H, dtype=dtype, device=device)
+    embedding = (torch.randn((vocab, H), generator=gen, device=device, dtype=torch.float32).to(dtype)
+                 if include_embedding else None)
+    lm_head = None
+    if include_lm_head:
+        if quantized_lm_head:
+            w, s, z = _random_linear(vocab, H, bits, group_size, gen, device, dtype)
+            lm_head = QuantizedHead(w, s, z, bits, group_size)
+        else:
+            lm_head = torch.randn((vocab, H), generator=gen, device=device, dtype=torch.float32).to(dtype)
+    return LlamaStackWeights(layers=layers, final_norm_weight=final_norm, lm_head=lm_head,
+                             embedding=embedding).validate(config)
+
+
+class DecodeGraph:
+    """One greedy decode step captured in a HIP graph: token ids [B] (int64,
+    device) at per-sequence positions [B] (int32, device) -> next token ids,
+    with every layer's cache written at those positions.  ``step()`` replays
+    the graph and advances the positions by one in place."""
+
+    def __init__(self, stack_weights: LlamaStackWeights, stack_cache: LlamaStackCache, cos, sin,
+                 config: LlamaLikeConfig, token_ids, positions):
+        if stack_weights.embedding is None or stack_weights.lm_head is None:
+            raise ValueError("DecodeGraph needs an embedding and an lm_head")
+        self.w, self.cache, self.cos, self.sin, self.config = stack_weights, stack_cache, cos, sin, config
+        self.tokens = token_ids.clone()
+        self.positions = positions.to(torch.int32).clone()
+        self.stream = torch.cuda.Stream(device=self.tokens.device)
+        self.stream.wait_stream(torch.cuda.current_stream(self.tokens.device))
+        with torch.cuda.stream(self.stream):
+            self._run()  # warm every cached buffer outside the capture
+        self.stream.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=self.stream):
+            self.next_tokens = self._run()
+
+    def _run(self):
+        x = embed_token_ids(self.tokens, self.w.embedding)
+        logits, _, _ = llama_stack_decode_step(x, self.w, self.cache, self.cos, self.sin, self.positions, self.config)
+        nxt = greedy_sample(logits)
+        self.tokens.copy_(nxt)
+        self.positions.add_(1)
+        return nxt
+
+    def step(self):
+        """Replays one step on the current stream: returns the next tokens
+        (the graph's output buffer, overwritten by the next step)."""
+        self.graph.replay()
+        return self.next_tokens

@@ -1,0 +1,225 @@
+"""Quantized paged decode block -- drop-in for the paged path of
+``ops/quantized_decode_block_ops.py``.
+
+One decode step of a layer's attention half on a paged fp16/bf16 KV cache
+(ops/quantized_decode_block_ops.py:446-552):
+    qkv = x . Wqkv^T            (q4/q8 matvec, mk_q{4,8}_matvec)
+    q, k, v = split(qkv); RoPE(q, k) at each sequence's position; the new k, v
+        written to (block_table[b, pos // P], pos % P)     (mk_qkv_rope_paged_update)
+    attn = paged GQA decode attention over positions 0..pos  (mk_paged_decode_attention)
+    projected = attn . Wo^T     (q4/q8 matvec)
+The cache is updated in place and returned, as the reference returns its
+updated copies.
+"""
+
+from __future__ import annotations
+
+import math
+
+from .gqa_ops import paged_gqa_decode_block_from_qkv, reference_paged_gqa_decode_block_from_qkv
+from .quant_ops import (
+    q4_matvec_decode,
+    q8_matvec_decode,
+    q_matvec_residual,
+    reference_q4_matvec_decode,
+    reference_q8_matvec_decode,
+)
+
+
+def validate_bits(bits: int) -> int:
+    """ops/quantized_decode_block_ops.py:20-23."""
+    if bits not in (4, 8):
+        raise ValueError(f"bits must be 4 or 8, got {bits}")
+    return bits
+
+
+def normalize_hidden_input(x):
+    """ops/quantized_decode_block_ops.py:26-37: [B,K], [B,1,K], [B,H,D] or
+    [B,1,H,D] -> ([B,K], B, original shape)."""
+    if x.ndim == 2:
+        return x, x.shape[0], tuple(x.shape)
+    if x.ndim == 3 and x.shape[1] == 1:
+        return x[:, 0, :], x.shape[0], tuple(x.shape)
+    if x.ndim == 3:
+        B = x.shape[0]
+        return x.reshape(B, x.shape[1] * x.shape[2]), B, tuple(x.shape)
+    if x.ndim == 4 and x.shape[1] == 1:
+        B = x.shape[0]
+        return x.reshape(B, x.shape[2] * x.shape[3]), B, tuple(x.shape)
+    raise ValueError(f"x must have shape [B,K], [B,1,K], [B,H,D], or [B,1,H,D], got {tuple(x.shape)}")
+
+
+def infer_gqa_qkv_output_dim(num_attention_heads: int, num_key_value_heads: int, head_dim: int) -> int:
+    """ops/quantized_decode_block_ops.py:65-66."""
+    return (num_attention_heads + 2 * num_key_value_heads) * head_dim
+
+
+def infer_qkv_dims(qkv_w, H, D, bits: int):
+    """ops/quantized_decode_block_ops.py:40-62 (fused MHA qkv: 3*H*D rows)."""
+    validate_bits(bits)
+    if qkv_w.ndim != 2:
+        raise ValueError(f"qkv_w must be 2-D, got {tuple(qkv_w.shape)}")
+    rows = qkv_w.shape[0]
+    if rows % 3 != 0:
+        raise ValueError(f"qkv_w output rows must be divisible by 3, got {rows}")
+    if H is not None and D is not None:
+        if 3 * H * D != rows:
+            raise ValueError(f"qkv_w output rows must equal 3*H*D={3 * H * D}, got {rows}")
+        return H, D
+    per = rows // 3
+    if H is not None:
+        if per % H != 0:
+            raise ValueError(f"qkv_w output rows imply per-projection dim {per}, not divisible by H={H}")
+        return H, per // H
+    if D is not None:
+        if per % D != 0:
+            raise ValueError(f"qkv_w output rows imply per-projection dim {per}, not divisible by D={D}")
+        return per // D, D
+    raise ValueError("H and D must be provided when qkv dimensions cannot be inferred uniquely")
+
+
+def validate_quantized_weight_shapes(x2d, w, scales, zeros, *, bits: int, group_size: int,
+                                     expected_in_dim: int | None = None, expected_out_dim: int | None = None,
+                                     name: str):
+    """ops/quantized_decode_block_ops.py:69-110 -> (in_dim, out_dim)."""
+    validate_bits(bits)
+    if group_size <= 0:
+        raise ValueError(f"group_size must be positive, got {group_size}")
+    if x2d.ndim != 2:
+        raise ValueError(f"{name} input must normalize to [B,K], got {tuple(x2d.shape)}")
+    if w.ndim != 2:
+        raise ValueError(f"{name} weights must be 2-D, got {tuple(w.shape)}")
+    in_dim = x2d.shape[1]
+    if expected_in_dim is not None and in_dim != expected_in_dim:
+        raise ValueError(f"{name} input dim must be {expected_in_dim}, got {in_dim}")
+    out_dim = w.shape[0]
+    if expected_out_dim is not None and out_dim != expected_out_dim:
+        raise ValueError(f"{name} output dim must be {expected_out_dim}, got {out_dim}")
+    if bits == 4:
+        packed = math.ceil(in_dim / 2)
+        if w.shape[1] != packed:
+            raise ValueError(f"{name} q4 weights must have shape [N,{packed}], got {tuple(w.shape)}")
+    elif w.shape[1] != in_dim:
+        raise ValueError(f"{name} q8 weights must have shape [N,{in_dim}], got {tuple(w.shape)}")
+    groups = math.ceil(in_dim / group_size)
+    if tuple(scales.shape) != (out_dim, groups):
+        raise ValueError(f"{name} scales must have shape {(out_dim, groups)}, got {tuple(scales.shape)}")
+    if zeros is not None and tuple(zeros.shape) != (out_dim, groups):
+        raise ValueError(f"{name} zeros must have shape {(out_dim, groups)}, got {tuple(zeros.shape)}")
+    return in_dim, out_dim
+
+
+def _matvec_dispatch(x2d, w, scales, zeros, *, bits: int, group_size: int, backend: str, reference: bool):
+    """ops/quantized_decode_block_ops.py:113-131."""
+    validate_bits(bits)
+    if reference:
+        fn = reference_q4_matvec_decode if bits == 4 else reference_q8_matvec_decode
+        return fn(x2d, w, scales, zeros, group_size=group_size)
+    fn = q4_matvec_decode if bits == 4 else q8_matvec_decode
+    return fn(x2d, w, scales, zeros, group_size=group_size, backend=backend)
+
+
+def quantized_qkv_projection(x, qkv_w, qkv_scales, qkv_zeros=None, *, bits=4, group_size=32, backend="auto"):
+    """ops/quantized_decode_block_ops.py:154-184 -> [B,1,N]."""
+    x2d, B, _ = normalize_hidden_input(x)
+    validate_quantized_weight_shapes(x2d, qkv_w, qkv_scales, qkv_zeros, bits=bits, group_size=group_size,
+                                     name="qkv_projection")
+    qkv = _matvec_dispatch(x2d, qkv_w, qkv_scales, qkv_zeros, bits=bits, group_size=group_size, backend=backend,
+                           reference=backend.lower() == "reference")
+    return qkv.reshape(B, 1, qkv.shape[1])
+
+
+def reference_quantized_qkv_projection(x, qkv_w, qkv_scales, qkv_zeros=None, *, bits=4, group_size=32):
+    """ops/quantized_decode_block_ops.py:134-151."""
+    return quantized_qkv_projection(x, qkv_w, qkv_scales, qkv_zeros, bits=bits, group_size=group_size,
+                                    backend="reference")
+
+
+def quantized_output_projection(x, out_w, out_scales, out_zeros=None, *, bits=4, group_size=32, backend="auto"):
+    """ops/quantized_decode_block_ops.py:207-237 -> [B,1,out]."""
+    x2d, B, _ = normalize_hidden_input(x)
+    _, out_dim = validate_quantized_weight_shapes(x2d, out_w, out_scales, out_zeros, bits=bits,
+                                                  group_size=group_size, name="output_projection")
+    y = _matvec_dispatch(x2d, out_w, out_scales, out_zeros, bits=bits, group_size=group_size, backend=backend,
+                         reference=backend.lower() == "reference")
+    return y.reshape(B, 1, out_dim)
+
+
+def reference_quantized_output_projection(x, out_w, out_scales, out_zeros=None, *, bits=4, group_size=32):
+    """ops/quantized_decode_block_ops.py:187-204."""
+    return quantized_output_projection(x, out_w, out_scales, out_zeros, bits=bits, group_size=group_size,
+                                       backend="reference")
+
+
+def _block_dims(qkv_w, H, num_key_value_heads, head_dim, D, bits):
+    """Head counts as ops/quantized_decode_block_ops.py:475-484 resolves them."""
+    if head_dim is not None:
+        D = head_dim
+    kv_heads = num_key_value_heads if num_key_value_heads is not None else H
+    if kv_heads is None:
+        H, D = infer_qkv_dims(qkv_w, H, D, bits)
+        kv_heads = H
+    elif H is None or D is None:
+        raise ValueError("H and head_dim/D are required for GQA paged quantized decode block")
+    return H, kv_heads, D
+
+
+def paged_quantized_decode_block(x, qkv_w, qkv_scales, out_w, out_scales, K_pages, V_pages, block_table, cos, sin,
+                                 position, *, qkv_zeros=None, out_zeros=None, bits=4, group_size=32, H=None,
+                                 num_key_value_heads=None, head_dim=None, D=None, scale=None,
+                                 matvec_backend="metal_parallel", block_backend="auto", return_intermediates=False,
+                                 residual=None):
+    """ops/quantized_decode_block_ops.py:446-552: returns (projected [B,1,H*D
+    -> hidden], K_pages, V_pages) or with (qkv, attn_out) appended.
+
+    ``residual`` (extension, not in the reference): when given, ``projected``
+    is residual + round(attn . Wo^T) from the matvec's residual epilogue --
+    the value the layer's following residual_add produces
+    (ops/llama_layer_ops.py:355-359) -- in the same launch."""
+    x2d, _, _ = normalize_hidden_input(x)
+    H, kv_heads, D = _block_dims(qkv_w, H, num_key_value_heads, head_dim, D, bits)
+    validate_quantized_weight_shapes(x2d, qkv_w, qkv_scales, qkv_zeros, bits=bits, group_size=group_size,
+                                     expected_out_dim=infer_gqa_qkv_output_dim(H, kv_heads, D),
+                                     name="qkv_projection")
+    validate_quantized_weight_shapes(x2d.new_empty((x2d.shape[0], H * D)), out_w, out_scales, out_zeros, bits=bits,
+                                     group_size=group_size, expected_in_dim=H * D, name="output_projection")
+    reference = matvec_backend.lower() == "reference"
+    qkv = quantized_qkv_projection(x2d, qkv_w, qkv_scales, qkv_zeros, bits=bits, group_size=group_size,
+                                   backend=matvec_backend)
+    block_fn = reference_paged_gqa_decode_block_from_qkv if block_backend.lower() == "reference" else None
+    if block_fn is not None:
+        attn_out, K_pages, V_pages = block_fn(qkv, K_pages, V_pages, block_table, cos, sin, position,
+                                              num_attention_heads=H, num_key_value_heads=kv_heads, head_dim=D,
+                                              scale=scale)
+    else:
+        attn_out, K_pages, V_pages = paged_gqa_decode_block_from_qkv(
+            qkv, K_pages, V_pages, block_table, cos, sin, position, num_attention_heads=H,
+            num_key_value_heads=kv_heads, head_dim=D, scale=scale, backend=block_backend)
+    B = attn_out.shape[0]
+    a2d = attn_out.reshape(B, H * D)
+    if residual is not None and not reference:
+        _, out = q_matvec_residual(a2d, out_w, out_scales, out_zeros, residual.reshape(B, -1), bits=bits,
+                                   group_size=group_size)
+        projected = out.reshape(B, 1, -1)
+    else:
+        projected = quantized_output_projection(a2d, out_w, out_scales, out_zeros, bits=bits, group_size=group_size,
+                                                backend=matvec_backend)
+        if residual is not None:
+            projected = (residual.reshape(B, 1, -1).float() + projected.float()).to(projected.dtype)
+    if return_intermediates:
+        return projected, K_pages, V_pages, qkv, attn_out
+    return projected, K_pages, V_pages
+
+
+def reference_paged_quantized_decode_block(x, qkv_w, qkv_scales, out_w, out_scales, K_pages, V_pages, block_table,
+                                           cos, sin, position, *, qkv_zeros=None, out_zeros=None, bits=4,
+                                           group_size=32, H=None, num_key_value_heads=None, head_dim=None, D=None,
+                                           scale=None, return_intermediates=False):
+    """ops/quantized_decode_block_ops.py:395-443 (reference matvecs and
+    reference paged block; K_pages / V_pages are updated functionally)."""
+    return paged_quantized_decode_block(
+        x, qkv_w, qkv_scales, out_w, out_scales, K_pages.clone(), V_pages.clone(), block_table, cos, sin, position,
+        qkv_zeros=qkv_zeros, out_zeros=out_zeros, bits=bits, group_size=group_size, H=H,
+        num_key_value_heads=num_key_value_heads, head_dim=head_dim, D=D, scale=scale, matvec_backend="reference",
+        block_backend="reference", return_intermediates=return_intermediates)
+

@@ -143,6 +143,32 @@ def test_mlp_block_zero_weights_is_residual_sum():
     assert np.array_equal(out, oq.residual_add(x, r))
 
 
+def test_decode_layer_zero_projections_is_identity():
+    """A layer whose projections all dequantize to 0 (codes at the zero
+    point) returns its input exactly and writes k = v = 0 at the new slot."""
+    from oracle import llama as ol
+
+    rng = np.random.default_rng(8)
+    B, H, Hq, Hkv, D, I, g, P, mb = 2, 64, 4, 2, 16, 128, 32, 4, 4
+    zero_pt = lambda n, k: (oq.pack_q4(np.full((n, k), 8, np.uint8)), np.ones((n, k // g), np.float32),
+                            np.full((n, k // g), 8.0, np.float32))
+    w = {"qkv": zero_pt((Hq + 2 * Hkv) * D, H), "o": zero_pt(H, Hq * D), "gate": zero_pt(I, H),
+         "up": zero_pt(I, H), "down": zero_pt(H, I), "ln1": np.ones(H, np.float16), "ln2": np.ones(H, np.float16)}
+    K = rng.standard_normal((B * mb, P, Hkv, D)).astype(np.float16)
+    V = rng.standard_normal((B * mb, P, Hkv, D)).astype(np.float16)
+    bt = np.arange(B * mb, dtype=np.int32).reshape(B, mb)
+    x = rng.standard_normal((B, H)).astype(np.float16)
+    cos, sin = op.rope_tables(64, D, 500000.0)
+    pos = [3, 9]
+    out, K2, V2 = ol.layer_decode_step(x, w, K, V, bt, cos, sin, pos, Hq, Hkv, D)
+    assert np.array_equal(out, x)
+    for b, p in enumerate(pos):
+        assert not K2[bt[b, p // P], p % P].any() and not V2[bt[b, p // P], p % P].any()
+    keep = np.ones(K.shape[:2], bool)
+    keep[[bt[b, p // P] for b, p in enumerate(pos)], [p % P for p in pos]] = False
+    assert np.array_equal(K2[keep], K[keep]) and np.array_equal(V2[keep], V[keep])
+
+
 # ------------------------------------------------------------ weight quantizer
 
 def test_weight_quantizer_reference_shapes_and_error():
