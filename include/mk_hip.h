@@ -129,6 +129,22 @@ int mk_q8_rmsnorm_gate_up(const void* x, const void* residual, const void* norm_
                           void* up_out, void* mlp_out, int64_t M, int64_t N, int64_t K, int64_t group_size,
                           int act_dtype, int scale_dtype, int norm_w_dtype, void* stream);
 
+/* RMSNorm + q4/q8 matvec: y = (x * rsqrt(mean(x^2) + eps) * norm_w, rounded
+ * to the activation dtype) . W^T -- the input norm and qkv projection of the
+ * decode layer (ops/llama_layer_ops.py:256-260 + ops/quantized_decode_block_ops.py:
+ * 154-184) and the final norm and head of the stack (ops/llama_stack_ops.py:
+ * 396-405).  x [M,K]; weights as mk_q4_matvec / mk_q8_matvec; y [M,N].
+ * For q4 with an M = 1 fp16 row, K <= 8192, fp16 norm weights and fp16
+ * scales this is one launch and normed_out [M,K] may be NULL; otherwise the
+ * norm kernel writes normed_out (then required) and the matvec reads it. */
+int mk_q4_rmsnorm_matvec(const void* x, const void* norm_w, float eps, const uint8_t* w, const void* scales,
+                         const void* zeros, void* normed_out, void* y, int64_t M, int64_t N, int64_t K,
+                         int64_t group_size, int act_dtype, int scale_dtype, int norm_w_dtype, void* stream);
+
+int mk_q8_rmsnorm_matvec(const void* x, const void* norm_w, float eps, const uint8_t* w, const void* scales,
+                         const void* zeros, void* normed_out, void* y, int64_t M, int64_t N, int64_t K,
+                         int64_t group_size, int act_dtype, int scale_dtype, int norm_w_dtype, void* stream);
+
 /* ---------------------------------------------------------------- elementwise / norm */
 
 /* swiglu / fused_swiglu -- ops/activation_ops.py:91-153.

@@ -201,8 +201,9 @@ struct GemvArgs {
   int rg;                // dot kernel: row groups per workgroup
   // residual + RMSNorm prologue (NORM dot kernels, M = 1): the product is
   // taken against n = fp16(z * rsqrt(mean(z^2) + eps) * nw), z = fp16(x +
-  // nres); workgroup 0 writes z and (when nout is given) n
-  const void* nres;      // [K]
+  // nres) (z = x when nres is null); workgroup 0 writes z and n when zout /
+  // nout are given
+  const void* nres;      // [K] or null
   const void* nw;        // [K] fp16
   void* zout;            // [K]
   void* nout;            // [K] or null
@@ -570,7 +571,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
   if constexpr (NORM) {
     const int c0 = threadIdx.x, c1 = two ? threadIdx.x + nthr : threadIdx.x;
     const int c1c = c1 < nchunk ? c1 : c0;
-    const f16* rp = reinterpret_cast<const f16*>(args.nres);
+    // no residual: the loads read x again and are dropped, so every load
+    // still issues in order
+    const f16* rp = reinterpret_cast<const f16*>(args.nres ? args.nres : args.x);
     const f16* wp = reinterpret_cast<const f16*>(args.nw);
     ax[0] = ldg128(x + 8 * c0);
     ax[1] = ldg128(x + 8 * c1c);
@@ -578,6 +581,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     ar[1] = ldg128(rp + 8 * c1c);
     aw[0] = ldg128(wp + 8 * c0);
     aw[1] = ldg128(wp + 8 * c1c);
+    if (!args.nres) ar[0] = ar[1] = (u32x4){0u, 0u, 0u, 0u};
   } else {
 #pragma unroll
     for (int j = 0; j < 4; ++j) f.x[j] = ldg128(x + k0 + 8 * j);
@@ -642,7 +646,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
         }
         *reinterpret_cast<u32x4*>(xrow + 8 * c) = nv;
         if (blockIdx.x == 0) {
-          *reinterpret_cast<u32x4*>(reinterpret_cast<f16*>(args.zout) + 8 * c) = zz[i];
+          if (args.zout) *reinterpret_cast<u32x4*>(reinterpret_cast<f16*>(args.zout) + 8 * c) = zz[i];
           if (args.nout) *reinterpret_cast<u32x4*>(reinterpret_cast<f16*>(args.nout) + 8 * c) = nv;
         }
       }
@@ -1083,9 +1087,66 @@ int norm_gate_up_entry(const void* x, const void* residual, const void* norm_w, 
                              sc_dt, stream);
 }
 
+// RMSNorm + matvec: y = fp16(x * rsqrt(mean(x^2) + eps) * norm_w) . W^T.
+// One launch (the norm as the dot kernel's prologue, no residual) for an
+// M = 1 fp16 q4 row the dot kernel takes, else the norm kernel into
+// normed_out and then the matvec.
+template <int BITS>
+int norm_matvec_entry(const void* x, const void* norm_w, float eps, const uint8_t* w, const void* s,
+                      const void* z, void* normed_out, void* y, int64_t M, int64_t N, int64_t K, int64_t gs,
+                      int act_dt, int sc_dt, int nw_dt, void* stream) {
+  MK_REQUIRE(x && norm_w && w && s && y);
+  MK_REQUIRE(M >= 0 && N > 0 && K > 0 && gs > 0 && N < (1LL << 31) && K < (1LL << 31));
+  MK_REQUIRE(act_dt == MK_DT_F16 || act_dt == MK_DT_BF16);
+  MK_REQUIRE(sc_dt == MK_DT_F16 || sc_dt == MK_DT_F32);
+  MK_REQUIRE(nw_dt == MK_DT_F16 || nw_dt == MK_DT_BF16 || nw_dt == MK_DT_F32);
+  if (M == 0) return MK_OK;
+  GemvArgs a = {};
+  a.x = x;
+  a.w[0] = a.w[1] = w;
+  a.s[0] = a.s[1] = s;
+  a.z[0] = a.z[1] = z;
+  a.y0 = y;
+  bool fast;
+  gemv_prepare<BITS, 1>(a, N, K, gs, &fast);
+  if constexpr (BITS == 4) {
+    // K <= 8192: the row fits two 16-byte chunks per thread of the workgroup
+    if (nw_dt == MK_DT_F16 && K <= 4 * 2048 && dot_eligible<BITS, 1>(a, fast && mk_aligned(x, 16), M, act_dt, sc_dt) &&
+        mk_aligned(norm_w, 16) && (!normed_out || mk_aligned(normed_out, 16))) {
+      a.M = 1;
+      a.kw = dot_waves(K);
+      a.nres = nullptr;
+      a.nw = norm_w;
+      a.zout = nullptr;
+      a.nout = normed_out;
+      a.eps = eps;
+      return launch_dot<BITS, 1, EPI_NONE, true>(a, reinterpret_cast<hipStream_t>(stream));
+    }
+  }
+  MK_REQUIRE(normed_out);  // the two-launch path passes the normalised rows through it
+  const int rc = mk_rms_norm(x, norm_w, normed_out, M, K, eps, act_dt, nw_dt, stream);
+  if (rc != MK_OK) return rc;
+  return matvec_entry<BITS>(normed_out, w, s, z, nullptr, nullptr, y, M, N, K, gs, act_dt, sc_dt, stream);
+}
+
 }  // namespace
 
 extern "C" {
+
+int mk_q4_rmsnorm_matvec(const void* x, const void* norm_w, float eps, const uint8_t* w, const void* scales,
+                         const void* zeros, void* normed_out, void* y, int64_t M, int64_t N, int64_t K,
+                         int64_t group_size, int act_dtype, int scale_dtype, int norm_w_dtype, void* stream) {
+  return norm_matvec_entry<4>(x, norm_w, eps, w, scales, zeros, normed_out, y, M, N, K, group_size, act_dtype,
+                              scale_dtype, norm_w_dtype, stream);
+}
+
+int mk_q8_rmsnorm_matvec(const void* x, const void* norm_w, float eps, const uint8_t* w, const void* scales,
+                         const void* zeros, void* normed_out, void* y, int64_t M, int64_t N, int64_t K,
+                         int64_t group_size, int act_dtype, int scale_dtype, int norm_w_dtype, void* stream) {
+  return norm_matvec_entry<8>(x, norm_w, eps, w, scales, zeros, normed_out, y, M, N, K, group_size, act_dtype,
+                              scale_dtype, norm_w_dtype, stream);
+}
+
 
 int mk_q4_matvec(const void* x, const uint8_t* w, const void* scales, const void* zeros,
                  const void* residual, void* y_mm, void* y_out, int64_t M, int64_t N, int64_t K,

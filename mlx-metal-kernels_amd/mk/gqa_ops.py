@@ -231,10 +231,12 @@ def _qkv_rope_update_prep(qkv, block_table, cos, sin, position, Hq, Hkv, D, page
 
 
 def paged_gqa_decode_block_from_qkv(qkv, K_pages, V_pages, block_table, cos, sin, position, *, num_attention_heads,
-                                    num_key_value_heads, head_dim, scale=None, backend="auto"):
+                                    num_key_value_heads, head_dim, scale=None, backend="auto", lengths=None):
     """ops/gqa_ops.py:493-547 as two HIP launches (fused split + RoPE +
     in-place paged update, then split-K GQA decode attention).  Returns
-    (out [B,1,Hq,D], K_pages, V_pages) like the reference."""
+    (out [B,1,Hq,D], K_pages, V_pages) like the reference.  ``lengths``
+    (extension): int32 [B] device tensor equal to position + 1, which a
+    caller running many layers at the same positions computes once."""
     backend_name = backend.lower()
     if backend_name not in ("auto", "reference", "metal", "metal_gqa", "metal_gqa_threadgroup"):
         raise ValueError("backend must be one of 'reference', 'metal', 'metal_gqa', 'metal_gqa_threadgroup', 'auto'")
@@ -261,5 +263,5 @@ def paged_gqa_decode_block_from_qkv(qkv, K_pages, V_pages, block_table, cos, sin
                 c.shape[0], _lib.dtype_code(K_pages.dtype))
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    out = _hip_paged_attention(q_out[:, 0], K_pages, V_pages, bt, pos + 1, scale)
+    out = _hip_paged_attention(q_out[:, 0], K_pages, V_pages, bt, pos + 1 if lengths is None else lengths, scale)
     return out.unsqueeze(1).to(qkv.dtype), K_pages, V_pages

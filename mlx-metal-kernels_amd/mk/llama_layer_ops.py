@@ -2,8 +2,8 @@
 ``ops/llama_layer_ops.py`` over torch tensors.
 
 One decode step of one layer (ops/llama_layer_ops.py:234-428):
-    x_norm = rms_norm(x, input_layernorm)                       mk_rms_norm
-    h = x + o_proj(attn(rope(split(qkv_proj(x_norm)))))          paged_quantized_decode_block
+    qkv = rms_norm(x, input_layernorm) . Wqkv^T                 mk_q{4,8}_rmsnorm_matvec
+    h = x + o_proj(attn(rope(split(qkv))))                       paged_quantized_decode_block
                                                                  (the residual add in the o-proj
                                                                   matvec's epilogue)
     out = quantized_mlp_block(h, 0, post_attention_layernorm)    mk_q{4,8}_rmsnorm_gate_up + down
@@ -178,20 +178,22 @@ def _check_decode(x, config: LlamaLikeConfig, cache, cache_layout: str):
 
 
 def llama_layer_decode_step(x, weights: LlamaLayerKernelWeights, cache, cos, sin, position, config,
-                            *, cache_layout: str = "paged", return_intermediates: bool = False):
+                            *, cache_layout: str = "paged", return_intermediates: bool = False, lengths=None):
     """ops/llama_layer_ops.py:234-428, paged layout, all stages on HIP.
     x [B,1,hidden]; cache (K_pages, V_pages, block_table) updated in place;
     position int or per-sequence [B].  Returns (out, cache) or
-    (out, cache, intermediates)."""
+    (out, cache, intermediates).  The input RMSNorm runs inside the qkv
+    matvec and the residual add inside the o-proj matvec; ``lengths``
+    (extension) = position + 1 as a device tensor shared by all layers."""
     config = config.validate()
     weights.validate(config)
     K_pages, V_pages, block_table = _check_decode(x, config, cache, cache_layout)
-    x_norm = rms_norm(x, weights.input_layernorm_weight, eps=config.rms_norm_eps)
     h, K_pages, V_pages, qkv, attn_out = paged_quantized_decode_block(
-        x_norm, weights.qkv_w, weights.qkv_scales, weights.o_w, weights.o_scales, K_pages, V_pages, block_table, cos,
+        x, weights.qkv_w, weights.qkv_scales, weights.o_w, weights.o_scales, K_pages, V_pages, block_table, cos,
         sin, position, qkv_zeros=weights.qkv_zeros, out_zeros=weights.o_zeros, bits=weights.bits,
         group_size=weights.group_size, H=config.num_attention_heads, num_key_value_heads=config.num_key_value_heads,
-        head_dim=config.head_dim, return_intermediates=True, residual=x)
+        head_dim=config.head_dim, return_intermediates=True, residual=x,
+        norm_weight=weights.input_layernorm_weight, eps=config.rms_norm_eps, lengths=lengths)
     res = quantized_mlp_block(h, _zero_residual(h), weights.post_attention_layernorm_weight, weights.gate_w,
                               weights.gate_scales, weights.up_w, weights.up_scales, weights.down_w, weights.down_scales,
                               gate_zeros=weights.gate_zeros, up_zeros=weights.up_zeros, down_zeros=weights.down_zeros,
@@ -201,6 +203,7 @@ def llama_layer_decode_step(x, weights: LlamaLayerKernelWeights, cache, cos, sin
     if not return_intermediates:
         return res, cache
     out, mi = res
+    x_norm = rms_norm(x, weights.input_layernorm_weight, eps=config.rms_norm_eps)
     return out, cache, {"x_norm": x_norm, "qkv": qkv, "attn_out": attn_out, "h": h, "mlp_norm": mi["normed"],
                         "gate": mi["gate"], "up": mi["up"], "mlp": mi["mlp"], "down": mi["down"]}
 

@@ -27,7 +27,7 @@ from .llama_layer_ops import (
     reference_llama_layer_decode_step,
 )
 from .norm_ops import reference_rms_norm, rms_norm
-from .quant_ops import q4_matvec_decode, q8_matvec_decode
+from .quant_ops import q4_matvec_decode, q8_matvec_decode, q_rmsnorm_matvec
 from .quantize_weights import QuantizationConfig, quantize_weight_groupwise
 
 
@@ -144,22 +144,40 @@ def llama_stack_decode_step(x, stack_weights: LlamaStackWeights, stack_cache: Ll
     (final_hidden, cache); with return_intermediates the per-layer hidden
     states are appended as a dict."""
     config = config.validate()
-    step = reference_llama_layer_decode_step if reference else llama_layer_decode_step
-    norm = reference_rms_norm if reference else rms_norm
     hidden = x
     layers_out = []
     new_caches = []
+    # every layer attends over positions 0..position: the lengths are shared
+    lengths = position.to(torch.int32) + 1 if isinstance(position, torch.Tensor) and position.is_cuda else None
     for li, lw in enumerate(stack_weights.layers):
-        hidden, cache = step(hidden, lw, stack_cache.layer_caches[li], cos, sin, position, config)
+        if reference:
+            hidden, cache = reference_llama_layer_decode_step(hidden, lw, stack_cache.layer_caches[li], cos, sin,
+                                                              position, config)
+        else:
+            hidden, cache = llama_layer_decode_step(hidden, lw, stack_cache.layer_caches[li], cos, sin, position,
+                                                    config, lengths=lengths)
         new_caches.append(cache)
         if return_intermediates:
             layers_out.append(hidden)
-    final_hidden = norm(hidden, stack_weights.final_norm_weight, eps=config.rms_norm_eps)
     cache = LlamaStackCache(new_caches, "paged", stack_cache.max_seq_len, stack_cache.page_size)
+    head = stack_weights.lm_head
+    logits = None
+    if isinstance(head, QuantizedHead) and not reference:
+        # final RMSNorm inside the head's matvec
+        B, T, H = hidden.shape
+        y, final_hidden = q_rmsnorm_matvec(hidden.reshape(B * T, H), stack_weights.final_norm_weight, head.w,
+                                           head.scales, head.zeros, bits=head.bits, group_size=head.group_size,
+                                           eps=config.rms_norm_eps, return_normed=True)
+        final_hidden = final_hidden.reshape(B, T, H)
+        logits = y.float().reshape(B, T, -1)
+    else:
+        norm = reference_rms_norm if reference else rms_norm
+        final_hidden = norm(hidden, stack_weights.final_norm_weight, eps=config.rms_norm_eps)
     inter = {"layers": layers_out, "final_hidden": final_hidden}
-    if stack_weights.lm_head is None:
+    if head is None:
         return (final_hidden, cache, inter) if return_intermediates else (final_hidden, cache)
-    logits = logits_from_hidden(final_hidden, stack_weights.lm_head)
+    if logits is None:
+        logits = logits_from_hidden(final_hidden, head)
     if return_intermediates:
         inter["logits"] = logits
         return logits, final_hidden, cache, inter

@@ -458,6 +458,42 @@ def q_rmsnorm_gate_up_swiglu(x, residual, norm_weight, gate_w, up_w, gate_scales
     return tuple(outs)
 
 
+def q_rmsnorm_matvec(x, norm_weight, w, scales, zeros=None, *, bits: int = 4, group_size: int = 32,
+                     eps: float = 1e-5, return_normed: bool = False):
+    """RMSNorm then the q4/q8 matvec, y = rms_norm(x) . W^T with the norm
+    rounded to x's dtype first (ops/norm_ops.py:47-52 feeding
+    ops/quant_ops.py:509-631) -- the decode layer's input norm + qkv
+    projection and the stack's final norm + head.  One HIP launch for a q4
+    fp16 decode row, the norm kernel then the matvec otherwise.  Returns y
+    [rows, N] (and the normalised rows with ``return_normed``)."""
+    x2d, original_shape, rows, k_dim = _normalize_hidden_rows_input(x)
+    _validate_matvec_input_dtype(x2d)
+    if tuple(norm_weight.shape) != (k_dim,):
+        raise ValueError(f"norm_weight must have shape {(k_dim,)}, got {tuple(norm_weight.shape)}")
+    if bits not in (4, 8):
+        raise ValueError(f"bits must be 4 or 8, got {bits}")
+    w8 = as_u8(w)
+    cols = math.ceil(k_dim / 2) if bits == 4 else k_dim
+    if w8.ndim != 2 or w8.shape[1] != cols:
+        raise ValueError(f"w must have shape [N,{cols}], got {tuple(w8.shape)}")
+    N = w8.shape[0]
+    _validate_group_params(N, k_dim, scales, zeros, group_size)
+    x2d = x2d.contiguous()
+    nw = norm_weight.contiguous()
+    dev = _lib.require_device(x2d, nw, w8, scales, zeros)
+    s, z = scales_for_kernel(scales, zeros)
+    normed = torch.empty_like(x2d)
+    y = torch.empty((rows, N), dtype=x2d.dtype, device=dev)
+    name = "mk_q4_rmsnorm_matvec" if bits == 4 else "mk_q8_rmsnorm_matvec"
+    _lib.launch(name, dev, _lib.ptr(x2d), _lib.ptr(nw), float(eps), _lib.ptr(w8), _lib.ptr(s), _lib.ptr(z),
+                _lib.ptr(normed), _lib.ptr(y), rows, N, k_dim, group_size, _lib.dtype_code(x2d.dtype),
+                _lib.dtype_code(s.dtype), _lib.dtype_code(nw.dtype))
+    y = _restore_hidden_rows_output(y, original_shape)
+    if return_normed:
+        return y, normed.reshape(x.shape)
+    return y
+
+
 def q_gate_up_swiglu(x, gate_w, up_w, gate_scales, up_scales, gate_zeros=None, up_zeros=None, *, bits: int = 4,
                      group_size: int = 32, return_gate_up: bool = False):
     """Gate/up projection with the SwiGLU epilogue fused in: silu(gate) * up

@@ -17,10 +17,12 @@ from __future__ import annotations
 import math
 
 from .gqa_ops import paged_gqa_decode_block_from_qkv, reference_paged_gqa_decode_block_from_qkv
+from .norm_ops import reference_rms_norm
 from .quant_ops import (
     q4_matvec_decode,
     q8_matvec_decode,
     q_matvec_residual,
+    q_rmsnorm_matvec,
     reference_q4_matvec_decode,
     reference_q8_matvec_decode,
 )
@@ -168,14 +170,17 @@ def paged_quantized_decode_block(x, qkv_w, qkv_scales, out_w, out_scales, K_page
                                  position, *, qkv_zeros=None, out_zeros=None, bits=4, group_size=32, H=None,
                                  num_key_value_heads=None, head_dim=None, D=None, scale=None,
                                  matvec_backend="metal_parallel", block_backend="auto", return_intermediates=False,
-                                 residual=None):
+                                 residual=None, norm_weight=None, eps=1e-5, lengths=None):
     """ops/quantized_decode_block_ops.py:446-552: returns (projected [B,1,H*D
     -> hidden], K_pages, V_pages) or with (qkv, attn_out) appended.
 
-    ``residual`` (extension, not in the reference): when given, ``projected``
-    is residual + round(attn . Wo^T) from the matvec's residual epilogue --
-    the value the layer's following residual_add produces
-    (ops/llama_layer_ops.py:355-359) -- in the same launch."""
+    Extensions, not in the reference, that let the layer fuse its
+    neighbours: ``residual`` makes ``projected`` residual + round(attn .
+    Wo^T) (the matvec's residual epilogue; the layer's residual_add,
+    ops/llama_layer_ops.py:355-359); ``norm_weight`` takes x before the
+    layer's input RMSNorm and runs the norm inside the qkv matvec
+    (ops/llama_layer_ops.py:256-260); ``lengths`` = position + 1 as a device
+    tensor, computed once for all layers."""
     x2d, _, _ = normalize_hidden_input(x)
     H, kv_heads, D = _block_dims(qkv_w, H, num_key_value_heads, head_dim, D, bits)
     validate_quantized_weight_shapes(x2d, qkv_w, qkv_scales, qkv_zeros, bits=bits, group_size=group_size,
@@ -184,8 +189,14 @@ def paged_quantized_decode_block(x, qkv_w, qkv_scales, out_w, out_scales, K_page
     validate_quantized_weight_shapes(x2d.new_empty((x2d.shape[0], H * D)), out_w, out_scales, out_zeros, bits=bits,
                                      group_size=group_size, expected_in_dim=H * D, name="output_projection")
     reference = matvec_backend.lower() == "reference"
-    qkv = quantized_qkv_projection(x2d, qkv_w, qkv_scales, qkv_zeros, bits=bits, group_size=group_size,
-                                   backend=matvec_backend)
+    if norm_weight is not None and not reference:
+        qkv = q_rmsnorm_matvec(x2d, norm_weight, qkv_w, qkv_scales, qkv_zeros, bits=bits, group_size=group_size,
+                               eps=eps).reshape(x2d.shape[0], 1, -1)
+    else:
+        if norm_weight is not None:
+            x2d = reference_rms_norm(x2d[:, None], norm_weight, eps=eps)[:, 0]
+        qkv = quantized_qkv_projection(x2d, qkv_w, qkv_scales, qkv_zeros, bits=bits, group_size=group_size,
+                                       backend=matvec_backend)
     block_fn = reference_paged_gqa_decode_block_from_qkv if block_backend.lower() == "reference" else None
     if block_fn is not None:
         attn_out, K_pages, V_pages = block_fn(qkv, K_pages, V_pages, block_table, cos, sin, position,
@@ -194,7 +205,7 @@ def paged_quantized_decode_block(x, qkv_w, qkv_scales, out_w, out_scales, K_page
     else:
         attn_out, K_pages, V_pages = paged_gqa_decode_block_from_qkv(
             qkv, K_pages, V_pages, block_table, cos, sin, position, num_attention_heads=H,
-            num_key_value_heads=kv_heads, head_dim=D, scale=scale, backend=block_backend)
+            num_key_value_heads=kv_heads, head_dim=D, scale=scale, backend=block_backend, lengths=lengths)
     B = attn_out.shape[0]
     a2d = attn_out.reshape(B, H * D)
     if residual is not None and not reference:

@@ -190,6 +190,32 @@ def test_rmsnorm_gate_up(dev, bits, rows, N, K, g, act):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("rows,N,K,g,act", [(1, 6144, 4096, 64, "f16"), (1, 512, 4096, 32, "f16"),
+                                            (1, 1000, 2048, 64, "f16"), (1, 300, 8192, 128, "f16"),
+                                            (2, 64, 256, 32, "f16"), (1, 64, 512, 64, "bf16")])
+def test_rmsnorm_matvec(dev, bits, rows, N, K, g, act):
+    """mk_q{4,8}_rmsnorm_matvec (one launch for a q4 fp16 row: the norm as the
+    dot kernel's prologue with no residual) against the norm kernel and the
+    oracle on the kernel's own normalised rows."""
+    import mk.norm_ops as norm
+
+    rng = np.random.default_rng(41 + rows + N + K)
+    _, stored, s, z = quant_weight(rng, N, K, g, bits, "sym")
+    xt, xf = _x(rng, rows, K, act, dev)
+    nw = torch.from_numpy((1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)).to(ACT[act]).to(dev)
+    y, normed = qo.q_rmsnorm_matvec(xt, nw, to_dev(stored, dev), to_dev(s, dev, torch.float16),
+                                    to_dev(z, dev, torch.float16), bits=bits, group_size=g, eps=1e-5,
+                                    return_normed=True)
+    n_ref = norm.rms_norm(xt[:, None], nw, eps=1e-5)[:, 0]
+    nd = (normed.float() - n_ref.float()).abs()
+    step = n_ref.float().abs() * (2.0 ** -10 if act == "f16" else 2.0 ** -7) + 1e-7
+    assert torch.all(nd <= step), "normed within one step of the norm kernel"
+    mv = oq.q4_matvec if bits == 4 else oq.q8_matvec
+    ref = mv(normed.float().cpu().numpy(), stored, s.astype(np.float16).astype(np.float32), z, g, act=act)
+    assert_close(y, ref, rtol=1e-2 if act == "f16" else 2e-2, what="rmsnorm matvec")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("preset", ["tiled", "fused_experimental", "parallel", "metal"])
 @pytest.mark.parametrize("B,S,D,I,g", [(1, 1, 64, 128, 32), (2, 1, 64, 130, 32), (1, 1, 4096, 14336, 64),
                                        (4, 1, 256, 512, 64)])
