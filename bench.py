@@ -49,6 +49,8 @@ def _parse():
     ap.add_argument("--sets", type=int, default=6, help="distinct weight sets rotated through (>= 512 MB total)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the M=4/8, q8 and attention extras")
+    ap.add_argument("--decode-stack-only", action="store_true",
+                    help="run only the config-5 decode stack extra and print its JSON (for profiling)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="first run a plain device copy of this many MiB (counter calibration)")
     ap.add_argument("--summarize-counters", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -384,6 +386,9 @@ def main():
     dev = torch.device("cuda:0")
     _lib.load()
     torch.manual_seed(0)
+    if args.decode_stack_only:
+        print(json.dumps(decode_stack_config5(dev)), flush=True)
+        return
     if args.calib_copy_mb:
         src = torch.empty(args.calib_copy_mb << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
