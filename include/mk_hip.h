@@ -147,6 +147,12 @@ int mk_q8_rmsnorm_matvec(const void* x, const void* norm_w, float eps, const uin
 
 /* ---------------------------------------------------------------- elementwise / norm */
 
+/* greedy_sample -- models/sampling.py:120-124 (np.argmax per row): out[r] = the
+ * index of the largest of x[r, 0..n), the first on ties, a NaN counting as
+ * the largest.  x [rows, n] f16/bf16/f32 (dtype), out int64 [rows]. */
+int mk_argmax_rows(const void* x, int64_t* out, int64_t rows, int64_t n, int dtype, void* stream);
+
+
 /* swiglu / fused_swiglu -- ops/activation_ops.py:91-153.
  * out = gate / (1 + exp(-gate)) * up, fp32 math, n elements. */
 int mk_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);

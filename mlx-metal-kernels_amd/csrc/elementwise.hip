@@ -209,9 +209,81 @@ int norm_entry(const void* x, const void* r, const void* w, void* z, void* y, in
   return MK_OK;
 }
 
+// Greedy sampling, models/sampling.py:120-124: per row the index of the
+// largest value, the first one on ties, a NaN counting as the largest (the
+// rule np.argmax follows).  One workgroup per row; threads scan 16-byte
+// chunks, then the (value, index) pairs reduce across lanes and waves.
+__device__ __forceinline__ bool argmax_better(float v, int64_t i, float bv, int64_t bi) {
+  if (bv != bv) return v != v && i < bi;
+  if (v != v) return true;
+  return v > bv || (v == bv && i < bi);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void argmax_rows_kernel(const T* __restrict__ x, int64_t* __restrict__ out,
+                                                          int64_t n, bool vec) {
+  const T* r = x + (size_t)blockIdx.x * n;
+  float bv = -INFINITY;
+  int64_t bi = n;  // no candidate yet: any real index is better on ties
+  if (vec) {
+    constexpr int EPC = 16 / sizeof(T);  // elements per 16-byte load
+    const int64_t nc = n / EPC;
+    for (int64_t c = threadIdx.x; c < nc; c += blockDim.x) {
+      const u32x4 w = ldg128(r + EPC * c);
+      T e[EPC];
+      __builtin_memcpy(e, &w, 16);
+#pragma unroll
+      for (int k = 0; k < EPC; ++k) {
+        const float v = to_f32(e[k]);
+        const int64_t i = EPC * c + k;
+        if (argmax_better(v, i, bv, bi)) { bv = v; bi = i; }
+      }
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+      const float v = to_f32(r[i]);
+      if (argmax_better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+  }
+  for (int d = 32; d >= 1; d >>= 1) {
+    const float ov = __shfl_xor(bv, d, 64);
+    const int64_t oi = __shfl_xor(bi, d, 64);
+    if (argmax_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  __shared__ float sv[4];
+  __shared__ int64_t si[4];
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { sv[wave] = bv; si[wave] = bi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+      if (argmax_better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
+    out[blockIdx.x] = bi < n ? bi : 0;
+  }
+}
+
 }  // namespace
 
 extern "C" {
+
+int mk_argmax_rows(const void* x, int64_t* out, int64_t rows, int64_t n, int dtype, void* stream) {
+  MK_REQUIRE(x && out && rows >= 0 && n > 0 && rows < (1LL << 31));
+  MK_REQUIRE(dtype == MK_DT_F16 || dtype == MK_DT_BF16 || dtype == MK_DT_F32);
+  if (rows == 0) return MK_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const size_t es = dtype == MK_DT_F32 ? 4 : 2;
+  // every row starts 16-byte aligned and holds whole 16-byte chunks
+  const bool vec = mk_aligned(x, 16) && ((size_t)n * es) % 16 == 0;
+  if (dtype == MK_DT_F16)
+    argmax_rows_kernel<f16><<<(unsigned)rows, 256, 0, st>>>((const f16*)x, out, n, vec);
+  else if (dtype == MK_DT_BF16)
+    argmax_rows_kernel<bf16><<<(unsigned)rows, 256, 0, st>>>((const bf16*)x, out, n, vec);
+  else
+    argmax_rows_kernel<float><<<(unsigned)rows, 256, 0, st>>>((const float*)x, out, n, vec);
+  MK_CHECK_LAUNCH();
+  return MK_OK;
+}
+
 
 int mk_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream) {
   MK_REQUIRE(gate && up && out && n >= 0);

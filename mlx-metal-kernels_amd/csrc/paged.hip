@@ -123,6 +123,64 @@ __global__ __launch_bounds__(256) void qkv_rope_update_kernel(
   for (int i = threadIdx.x; i < Hkv * D; i += blockDim.x) Vp[dst + i] = vrow[i];
 }
 
+// Vectorised form of qkv_rope_update_kernel for D % 8 == 0 and 16-byte
+// aligned rows: one thread per 8 elements (four RoPE pairs, one 16-byte load
+// and store), the q, k and v tasks of a sequence spread over
+// ceil(tasks / 128) workgroups so a small batch still fills several CUs.
+// Same arithmetic and the same skip rules as the scalar kernel.
+template <typename T>
+__global__ __launch_bounds__(128) void qkv_rope_update_vec_kernel(
+    const T* __restrict__ qkv, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    const int32_t* __restrict__ pos, const int32_t* __restrict__ bt, T* __restrict__ Kp,
+    T* __restrict__ Vp, T* __restrict__ q_out, int B, int Hq, int Hkv, int D, int P,
+    int max_blocks, int num_pages, int cos_rows) {
+  const int b = blockIdx.x;
+  const int cpr = D / 8;  // 8-element chunks per head row
+  const int nq = Hq * cpr, nk = Hkv * cpr;
+  const int t = (int)blockIdx.y * 128 + (int)threadIdx.x;
+  if (t >= nq + 2 * nk) return;
+  const int p = pos[b];
+  if (p < 0 || p >= cos_rows) return;
+  const T* row = qkv + (size_t)b * (Hq + 2 * Hkv) * D;
+  if (t < nq + nk) {
+    const bool isq = t < nq;
+    const int tt = isq ? t : t - nq;
+    const int h = tt / cpr, c = tt - h * cpr;
+    const u32x4 xv = ldg128(row + (isq ? 0 : (size_t)Hq * D) + (size_t)h * D + 8 * c);
+    const u32x4 cv = ldg128(cos_t + (size_t)p * (D / 2) + 4 * c);
+    const u32x4 sv = ldg128(sin_t + (size_t)p * (D / 2) + 4 * c);
+    T xe[8], ye8[8];
+    float ce[4], se[4];
+    __builtin_memcpy(xe, &xv, 16);
+    __builtin_memcpy(ce, &cv, 16);
+    __builtin_memcpy(se, &sv, 16);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float ye, yo;
+      rope_pair(to_f32(xe[2 * e]), to_f32(xe[2 * e + 1]), ce[e], se[e], &ye, &yo);
+      ye8[2 * e] = from_f32<T>(ye);
+      ye8[2 * e + 1] = from_f32<T>(yo);
+    }
+    u32x4 yv;
+    __builtin_memcpy(&yv, ye8, 16);
+    if (isq) {
+      *reinterpret_cast<u32x4*>(q_out + ((size_t)b * Hq + h) * D + 8 * c) = yv;
+      return;
+    }
+    int off;
+    const int page = slot_page(bt, pos, b, max_blocks, P, num_pages, &off);
+    if (page < 0 || superseded(bt, pos, b, B, max_blocks, P, num_pages, page, off)) return;
+    *reinterpret_cast<u32x4*>(Kp + ((size_t)page * P + off) * Hkv * D + (size_t)h * D + 8 * c) = yv;
+    return;
+  }
+  const int tt = t - nq - nk;  // v chunk
+  int off;
+  const int page = slot_page(bt, pos, b, max_blocks, P, num_pages, &off);
+  if (page < 0 || superseded(bt, pos, b, B, max_blocks, P, num_pages, page, off)) return;
+  *reinterpret_cast<u32x4*>(Vp + ((size_t)page * P + off) * Hkv * D + 8 * (size_t)tt) =
+      ldg128(row + (size_t)(Hq + Hkv) * D + 8 * (size_t)tt);
+}
+
 // Quantized variant.  LDS holds the rounded k_rope / v (as fp32) and the
 // codes; one wave quantizes one (K|V, head, group) at a time.
 constexpr int QUPD_MAX_ELEMS = 4096;  // Hkv * D per K or V
@@ -329,6 +387,22 @@ int mk_qkv_rope_paged_update(const void* qkv, const float* cos_t, const float* s
   MK_REQUIRE(dtype == MK_DT_F16 || dtype == MK_DT_BF16);
   if (B == 0) return MK_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int64_t tasks = (Hq + 2 * Hkv) * (D / 8);
+  if ((D % 8) == 0 && tasks <= 65535LL * 128 && mk_aligned(qkv, 16) && mk_aligned(q_out, 16) &&
+      mk_aligned(K_pages, 16) && mk_aligned(V_pages, 16) && mk_aligned(cos_t, 16) &&
+      mk_aligned(sin_t, 16)) {
+    const dim3 grid((unsigned)B, (unsigned)((tasks + 127) / 128));
+#define MK_QRV(T)                                                                                 \
+  qkv_rope_update_vec_kernel<T><<<grid, 128, 0, st>>>(                                            \
+      (const T*)qkv, cos_t, sin_t, positions, block_table, (T*)K_pages, (T*)V_pages, (T*)q_out, \
+      (int)B, (int)Hq, (int)Hkv, (int)D, (int)page_size, (int)max_blocks, (int)num_pages,        \
+      (int)cos_rows)
+    if (dtype == MK_DT_F16) MK_QRV(f16);
+    else MK_QRV(bf16);
+#undef MK_QRV
+    MK_CHECK_LAUNCH();
+    return MK_OK;
+  }
 #define MK_QRU(T)                                                                                 \
   qkv_rope_update_kernel<T><<<(unsigned)B, 256, 0, st>>>(                                         \
       (const T*)qkv, cos_t, sin_t, positions, block_table, (T*)K_pages, (T*)V_pages, (T*)q_out, \

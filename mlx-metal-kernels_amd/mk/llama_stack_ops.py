@@ -20,6 +20,7 @@ from typing import Any
 
 import torch
 
+from . import _lib
 from .llama_layer_ops import (
     LlamaLayerKernelWeights,
     LlamaLikeConfig,
@@ -132,17 +133,29 @@ def logits_from_hidden(hidden, lm_head):
 
 
 def greedy_sample(logits):
-    """models/sampling.py:120-124: argmax over the vocabulary (first index on
-    ties) -> int64 [B]."""
-    return torch.argmax(logits.reshape(logits.shape[0], -1), dim=-1)
+    """models/sampling.py:120-124: argmax over the vocabulary -> int64 [B],
+    with np.argmax's rule (the first index on ties, a NaN wins).  Device
+    logits (fp16/bf16/fp32) go to the HIP row argmax, host ones to torch."""
+    rows = logits.reshape(logits.shape[0], -1)
+    if not rows.is_cuda:
+        return torch.argmax(rows, dim=-1)
+    rows = rows.contiguous()
+    dev = _lib.require_device(rows)
+    out = torch.empty(rows.shape[0], dtype=torch.int64, device=rows.device)
+    _lib.launch("mk_argmax_rows", dev, _lib.ptr(rows), _lib.ptr(out), rows.shape[0], rows.shape[1],
+                _lib.dtype_code(rows.dtype))
+    return out
 
 
 def llama_stack_decode_step(x, stack_weights: LlamaStackWeights, stack_cache: LlamaStackCache, cos, sin, position,
-                            config: LlamaLikeConfig, *, return_intermediates: bool = False, reference: bool = False):
+                            config: LlamaLikeConfig, *, return_intermediates: bool = False, reference: bool = False,
+                            float_logits: bool = True):
     """ops/llama_stack_ops.py:352-411 on paged caches.  Returns (logits,
     final_hidden, cache) when the weights carry an lm_head, else
     (final_hidden, cache); with return_intermediates the per-layer hidden
-    states are appended as a dict."""
+    states are appended as a dict.  Logits are fp32; ``float_logits=False``
+    keeps a quantized head's logits in the activation dtype (the widening is
+    exact, so an argmax over either agrees)."""
     config = config.validate()
     hidden = x
     layers_out = []
@@ -169,7 +182,7 @@ def llama_stack_decode_step(x, stack_weights: LlamaStackWeights, stack_cache: Ll
                                            head.scales, head.zeros, bits=head.bits, group_size=head.group_size,
                                            eps=config.rms_norm_eps, return_normed=True)
         final_hidden = final_hidden.reshape(B, T, H)
-        logits = y.float().reshape(B, T, -1)
+        logits = (y.float() if float_logits else y).reshape(B, T, -1)
     else:
         norm = reference_rms_norm if reference else rms_norm
         final_hidden = norm(hidden, stack_weights.final_norm_weight, eps=config.rms_norm_eps)
@@ -254,7 +267,8 @@ class DecodeGraph:
 
     def _run(self):
         x = embed_token_ids(self.tokens, self.w.embedding)
-        logits, _, _ = llama_stack_decode_step(x, self.w, self.cache, self.cos, self.sin, self.positions, self.config)
+        logits, _, _ = llama_stack_decode_step(x, self.w, self.cache, self.cos, self.sin, self.positions, self.config,
+                                               float_logits=False)
         nxt = greedy_sample(logits)
         self.tokens.copy_(nxt)
         self.positions.add_(1)

@@ -80,3 +80,32 @@ def test_swiglu_and_residual_add(dev, n, dt):
     assert_close(got.float().cpu().numpy(), ref, what="swiglu")
     s = fused.residual_add(g, u)
     assert np.array_equal(s.float().cpu().numpy(), _round(gf + uf, dt))
+
+
+@pytest.mark.parametrize("rows,n,dt", [(1, 128256, torch.float16), (32, 128256, torch.float16),
+                                       (3, 1000, torch.bfloat16), (2, 515, torch.float16),
+                                       (4, 4096, torch.float32), (2, 7, torch.float32)])
+def test_argmax_rows(dev, rows, n, dt):
+    """Greedy sampling (models/sampling.py:120-124) on device against
+    np.argmax: random rows, planted ties (the first index must win) and a NaN
+    row (the first NaN wins, as in numpy)."""
+    from mk.llama_stack_ops import greedy_sample
+
+    rng = np.random.default_rng(rows * 7 + n)
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    if rows > 1:  # a tie between two positions of the row's maximum
+        x[1, n // 3] = x[1, n - 1] = x[1].max() + 1.0
+    if rows > 2:
+        x[2, n // 2] = np.nan
+        x[2, n - 2] = np.nan
+    xt = torch.from_numpy(x).to(dt)
+    want = np.argmax(xt.float().numpy(), axis=-1)  # the rounded values' argmax
+    got = greedy_sample(xt.to(dev)).cpu().numpy()
+    assert got.dtype == np.int64
+    assert np.array_equal(got, want), (got, want)
+    # a 3-D [B, 1, vocab] input and a misaligned (offset) view take the same answer
+    got3 = greedy_sample(xt.to(dev)[:, None]).cpu().numpy()
+    assert np.array_equal(got3, want)
+    if n > 1:
+        xs = xt.to(dev)[:, 1:]
+        assert np.array_equal(greedy_sample(xs).cpu().numpy(), np.argmax(xt.float().numpy()[:, 1:], axis=-1))
