@@ -6,6 +6,9 @@
 // q4 codes are packed two per byte (low nibble = even k), so on little-endian
 // hardware a 32-bit word holds 8 consecutive codes, nibble i at bits 4i.
 //
+// Decode batches of at most 4 rows (q8: 2) with fp16 activations and scales
+// take the v_dot2 kernel below; larger batches, bf16 and fp32 scales the
+// MFMA path:
 // Fast path (M <= 16 per launch, K % 64 == 0 for q4 / % 32 for q8, power-of-two
 // group size >= 16 (q4) / >= 8 (q8)):
 //   * one workgroup owns a 16-row output tile; its KW waves split K;
@@ -16,8 +19,10 @@
 //   * the waves' partial 16x16 tiles are summed through LDS; the epilogue
 //     saturates, and optionally fuses SwiGLU (gate/up) or a residual add.
 // fp16 activations with fp16 scales use an exponent-magic dequant: a code c
-// OR'ed into the mantissa of 1024.0h gives 1024+c exactly, so
-//   w = fma(c, s, -z*s)  (two packed-f16 ops per pair of weights).
+// OR'ed into the mantissa of 1024.0h gives 1024+c exactly, so with zi the
+// rounded zero point
+//   w = fma((1024 + c) - (1024 + zi), s, -(z - zi) s)  (two packed-f16 ops
+// per pair of weights; one rounding for integer zero points).
 // The MFMA contraction is order-free in k, so the activation operand is built
 // in the same permuted k order the magic unpack produces.
 #include "common.h"
@@ -63,11 +68,18 @@ __device__ __forceinline__ u32x4 xperm(u32x4 X) {
   }
 }
 
-// Per-group dequant parameters.
+// Per-group dequant parameters.  The integer part zi of the zero point is
+// subtracted exactly from the magic-biased codes ((1024 + c) - (1024 + zi) =
+// c - zi, exact in fp16 for |zi| < 64 (q4 high nibbles: 16 zi) / 1024 (q8)),
+// so w = fma(c - zi, s, corr) with corr = -(z - zi) s rounds once, to the
+// fp16 of (c - z) s whenever z is an integer -- the rounding of the
+// reference's fp32 dequant -- and keeps a fractional z exact to ulp(corr).
 struct GpMagic {
-  f16x2 s;    // (s, s)
-  f16x2 s16;  // (s/16, s/16)  for codes sitting at nibble bits 4..7
-  f16x2 nzs;  // (-z*s, -z*s)
+  f16x2 s;     // (s, s)
+  f16x2 s16;   // (s/16, s/16)  for codes sitting at nibble bits 4..7
+  f16x2 kz;    // (1024 + zi)
+  f16x2 kz16;  // (1024 + 16 zi)
+  f16x2 corr;  // -(z - zi) * s
 };
 struct GpExact {
   float s;
@@ -78,25 +90,28 @@ __device__ __forceinline__ f16x2 h2(f16 v) { return (f16x2){v, v}; }
 
 __device__ __forceinline__ GpMagic make_gp_magic(f16 s, f16 z) {
   GpMagic g;
+  const float zf = (float)z;
+  const float zi = rintf(zf);
   g.s = h2(s);
   g.s16 = h2(s * (f16)0.0625f);
-  g.nzs = h2(-(z * s));
+  g.kz = h2((f16)(1024.0f + zi));
+  g.kz16 = h2((f16)(1024.0f + 16.0f * zi));
+  g.corr = h2((f16)(-(zf - zi) * (float)s));
   return g;
 }
 
 // q4 word (8 codes) -> 8 fp16 weights in order [0,4,1,5,2,6,3,7].
 // `magic` = 0x64006400 held in a VGPR so each unpack is one v_and_or_b32.
 __device__ __forceinline__ u32x4 dq4_magic(uint32_t u, const GpMagic& g, uint32_t magic) {
-  const f16x2 k1024 = {(f16)1024.0f, (f16)1024.0f};
   const uint32_t v = u >> 8;
-  f16x2 a = bitcast<f16x2>((u & 0x000F000Fu) | magic) - k1024;  // c0, c4
-  f16x2 b = bitcast<f16x2>((u & 0x00F000F0u) | magic) - k1024;  // 16*c1, 16*c5
-  f16x2 c = bitcast<f16x2>((v & 0x000F000Fu) | magic) - k1024;  // c2, c6
-  f16x2 d = bitcast<f16x2>((v & 0x00F000F0u) | magic) - k1024;  // 16*c3, 16*c7
-  a = __builtin_elementwise_fma(a, g.s, g.nzs);
-  b = __builtin_elementwise_fma(b, g.s16, g.nzs);
-  c = __builtin_elementwise_fma(c, g.s, g.nzs);
-  d = __builtin_elementwise_fma(d, g.s16, g.nzs);
+  f16x2 a = bitcast<f16x2>((u & 0x000F000Fu) | magic) - g.kz;    // c0 - zi, c4 - zi
+  f16x2 b = bitcast<f16x2>((u & 0x00F000F0u) | magic) - g.kz16;  // 16 (c1 - zi), 16 (c5 - zi)
+  f16x2 c = bitcast<f16x2>((v & 0x000F000Fu) | magic) - g.kz;    // c2, c6
+  f16x2 d = bitcast<f16x2>((v & 0x00F000F0u) | magic) - g.kz16;  // 16 c3, 16 c7
+  a = __builtin_elementwise_fma(a, g.s, g.corr);
+  b = __builtin_elementwise_fma(b, g.s16, g.corr);
+  c = __builtin_elementwise_fma(c, g.s, g.corr);
+  d = __builtin_elementwise_fma(d, g.s16, g.corr);
   u32x4 r;
   r[0] = bitcast<uint32_t>(a);
   r[1] = bitcast<uint32_t>(b);
@@ -118,15 +133,14 @@ __device__ __forceinline__ uint32_t q8_hi_pair(uint32_t u, uint32_t magic8) {
 // two q8 words (8 codes) -> 8 fp16 weights in order [0,2,1,3,4,6,5,7].
 __device__ __forceinline__ u32x4 dq8_magic(uint32_t u0, uint32_t u1, const GpMagic& g,
                                            uint32_t magic8) {
-  const f16x2 k1024 = {(f16)1024.0f, (f16)1024.0f};
-  f16x2 a0 = bitcast<f16x2>(q8_lo_pair(u0, magic8)) - k1024;
-  f16x2 b0 = bitcast<f16x2>(q8_hi_pair(u0, magic8)) - k1024;
-  f16x2 a1 = bitcast<f16x2>(q8_lo_pair(u1, magic8)) - k1024;
-  f16x2 b1 = bitcast<f16x2>(q8_hi_pair(u1, magic8)) - k1024;
-  a0 = __builtin_elementwise_fma(a0, g.s, g.nzs);
-  b0 = __builtin_elementwise_fma(b0, g.s, g.nzs);
-  a1 = __builtin_elementwise_fma(a1, g.s, g.nzs);
-  b1 = __builtin_elementwise_fma(b1, g.s, g.nzs);
+  f16x2 a0 = bitcast<f16x2>(q8_lo_pair(u0, magic8)) - g.kz;
+  f16x2 b0 = bitcast<f16x2>(q8_hi_pair(u0, magic8)) - g.kz;
+  f16x2 a1 = bitcast<f16x2>(q8_lo_pair(u1, magic8)) - g.kz;
+  f16x2 b1 = bitcast<f16x2>(q8_hi_pair(u1, magic8)) - g.kz;
+  a0 = __builtin_elementwise_fma(a0, g.s, g.corr);
+  b0 = __builtin_elementwise_fma(b0, g.s, g.corr);
+  a1 = __builtin_elementwise_fma(a1, g.s, g.corr);
+  b1 = __builtin_elementwise_fma(b1, g.s, g.corr);
   u32x4 r;
   r[0] = bitcast<uint32_t>(a0);
   r[1] = bitcast<uint32_t>(b0);
@@ -384,10 +398,15 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(const GemvArgs args) {
 }
 
 // --------------------------------------------------------------------------
-// M = 1 kernel: v_dot2_f32_f16 on (nearly) raw codes.
+// M <= 4 kernel: v_dot2_f32_f16 on (nearly) raw codes.
 //
 // A lane handles 32-k "units" (16 code bytes for q4, 32 for q8) of R output
-// rows (x NMAT matrices); the R rows share the lane's x registers.  The codes
+// rows (x NMAT matrices); the R rows share the lane's x registers, and with
+// several activation rows (a small decode batch) every row's dot products
+// reuse the same unpacked codes -- 4 v_dot2 per 8 codes and row against a
+// 5-instruction unpack, where the MFMA path spends 13 instructions per 8
+// codes on dequantization and at M <= 4 uses at most a quarter of each
+// 16-column product.  The codes
 // are never scaled: the exponent-magic trick turns each code pair into an
 // fp16 pair, v_dot2 accumulates x . code in fp32, and the group's affine map
 // is applied once per unit in fp32:
@@ -466,10 +485,10 @@ __device__ __forceinline__ void reduce_scatter(float* v, int lane) {
   }
 }
 
-template <int BITS, int NMAT, int R>
+template <int BITS, int NMAT, int R, int MR>
 struct DotFrag {
   u32x4 w[NMAT][R][BITS == 4 ? 1 : 2];
-  u32x4 x[4];
+  u32x4 x[MR][4];
 };
 
 // Full 64-lane sum, in every lane.
@@ -489,11 +508,16 @@ __device__ __forceinline__ float wave_total(float v) {
 // thread, normalises the row into LDS, and every wave reads its slice from
 // there: two row groups share that work, and the activation traffic per
 // code byte is what keeps the prologue cheap.
-template <int BITS, int NMAT, int EPI, bool NORM>
+// MR activation rows (1, 2 or 4; rows past M repeat row M - 1 and are not
+// stored) share each lane's code unpack: a batched decode step costs 4 MR
+// v_dot2 per 8 codes on top of the 5-instruction unpack.
+template <int BITS, int NMAT, int EPI, bool NORM, int MR>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void gemv_dot_kernel(
     const GemvArgs args) {
+  static_assert(!NORM || MR == 1, "the norm prologue takes one activation row");
   constexpr int R = dot_rows<BITS, NMAT>();
-  constexpr int V = NMAT * R;  // values reduced per lane
+  constexpr int V = NMAT * R;  // values per activation row reduced per lane
+  constexpr int VT = V * MR;   // values reduced per lane
   constexpr int NSEG = V * 2;  // (matrix, row, s|z) runs staged per wave
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -565,7 +589,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
   const int nchunk = K / 8;
   const bool two = nthr < nchunk;  // workgroup-uniform
   u32x4 ax[NORM ? 2 : 1], ar[NORM ? 2 : 1], aw[NORM ? 2 : 1];
-  DotFrag<BITS, NMAT, R> f;
+  DotFrag<BITS, NMAT, R, MR> f;
   const int u = ubase + lane;
   const int k0 = (u < U ? u : 0) * 32;
   if constexpr (NORM) {
@@ -584,7 +608,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     if (!args.nres) ar[0] = ar[1] = (u32x4){0u, 0u, 0u, 0u};
   } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) f.x[j] = ldg128(x + k0 + 8 * j);
+    for (int m = 0; m < MR; ++m) {
+      const f16* xm = x + (size_t)(m < args.M ? m : args.M - 1) * K;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) f.x[m][j] = ldg128(xm + k0 + 8 * j);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);  // the activation loads stay ahead of the codes
 #pragma unroll
@@ -653,28 +681,33 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     }
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 4; ++j) f.x[j] = *reinterpret_cast<const u32x4*>(xrow + k0 + 8 * j);
+    for (int j = 0; j < 4; ++j) f.x[0][j] = *reinterpret_cast<const u32x4*>(xrow + k0 + 8 * j);
   } else {
     __builtin_amdgcn_wave_barrier();
   }
 
-  float acc[V];
+  float acc[VT];  // index m * V + t * R + r
 #pragma unroll
-  for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+  for (int i = 0; i < VT; ++i) acc[i] = 0.0f;
 
   {  // one 64-unit slice per wave (the dispatcher guarantees U <= 64 * kw)
     // a lane past the last unit computes on x = 0: its codes, offsets and
     // zero-point terms all vanish, so its sums add nothing
     if (u >= U) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) f.x[j] = (u32x4){0u, 0u, 0u, 0u};
+      for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f.x[m][j] = (u32x4){0u, 0u, 0u, 0u};
     }
 
-    // activation operands in the unpack order, and their sums
-    uint32_t xp[16];
+    // activation operands in the unpack order, and their sums, per row m
+    uint32_t xp[MR][16];
+    float xsm[MR], nboff[MR];
+    const uint32_t one2 = 0x3C003C00u;  // (1.0h, 1.0h)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
     float xs = 0.0f;  // X, the sum of the slice's x
     float boff;       // what the exponent-magic offsets add to the code sums
-    const uint32_t one2 = 0x3C003C00u;  // (1.0h, 1.0h)
     if constexpr (BITS == 4) {
       // low nibbles decode to 1024 + c, high nibbles (in place) to
       // 1024 + 16 c against x / 16: the offsets sum to 1024 X_lo + 64 X_hi
@@ -683,16 +716,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         // word j covers x[8j .. 8j+8): pairs (0,4) (1,5)/16 (2,6) (3,7)/16
-        const uint32_t p0 = pack_lo16(f.x[j][0], f.x[j][2]);
-        const uint32_t p1 = pack_hi16(f.x[j][0], f.x[j][2]);
-        const uint32_t p2 = pack_lo16(f.x[j][1], f.x[j][3]);
-        const uint32_t p3 = pack_hi16(f.x[j][1], f.x[j][3]);
+        const uint32_t p0 = pack_lo16(f.x[m][j][0], f.x[m][j][2]);
+        const uint32_t p1 = pack_hi16(f.x[m][j][0], f.x[m][j][2]);
+        const uint32_t p2 = pack_lo16(f.x[m][j][1], f.x[m][j][3]);
+        const uint32_t p3 = pack_hi16(f.x[m][j][1], f.x[m][j][3]);
         xs_hi = dot2(p1, one2, dot2(p3, one2, xs_hi));
         xs_lo = dot2(p0, one2, dot2(p2, one2, xs_lo));
-        xp[4 * j + 0] = p0;
-        xp[4 * j + 1] = bitcast<uint32_t>(bitcast<f16x2>(p1) * sixteenth);
-        xp[4 * j + 2] = p2;
-        xp[4 * j + 3] = bitcast<uint32_t>(bitcast<f16x2>(p3) * sixteenth);
+        xp[m][4 * j + 0] = p0;
+        xp[m][4 * j + 1] = bitcast<uint32_t>(bitcast<f16x2>(p1) * sixteenth);
+        xp[m][4 * j + 2] = p2;
+        xp[m][4 * j + 3] = bitcast<uint32_t>(bitcast<f16x2>(p3) * sixteenth);
       }
       xs = xs_lo + xs_hi;
       boff = 1024.0f * xs_lo + 64.0f * xs_hi;
@@ -700,16 +733,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         // two words per 8 x's: pairs (0,2) (1,3) (4,6) (5,7)
-        xp[4 * j + 0] = pack_lo16(f.x[j][0], f.x[j][1]);
-        xp[4 * j + 1] = pack_hi16(f.x[j][0], f.x[j][1]);
-        xp[4 * j + 2] = pack_lo16(f.x[j][2], f.x[j][3]);
-        xp[4 * j + 3] = pack_hi16(f.x[j][2], f.x[j][3]);
-        xs = dot2(xp[4 * j + 0], one2, dot2(xp[4 * j + 1], one2,
-                  dot2(xp[4 * j + 2], one2, dot2(xp[4 * j + 3], one2, xs))));
+        xp[m][4 * j + 0] = pack_lo16(f.x[m][j][0], f.x[m][j][1]);
+        xp[m][4 * j + 1] = pack_hi16(f.x[m][j][0], f.x[m][j][1]);
+        xp[m][4 * j + 2] = pack_lo16(f.x[m][j][2], f.x[m][j][3]);
+        xp[m][4 * j + 3] = pack_hi16(f.x[m][j][2], f.x[m][j][3]);
+        xs = dot2(xp[m][4 * j + 0], one2, dot2(xp[m][4 * j + 1], one2,
+                  dot2(xp[m][4 * j + 2], one2, dot2(xp[m][4 * j + 3], one2, xs))));
       }
       boff = 1024.0f * xs;
     }
-    const float nboff = -boff;
+    xsm[m] = xs;
+    nboff[m] = -boff;
+    }
     // this lane's group within the wave's slice; run seg is at seg * 64
     const f16* szl = reinterpret_cast<const f16*>(stage) + ((lane * 32) >> args.lg);
 
@@ -717,52 +752,67 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     for (int t = 0; t < NMAT; ++t)
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        float tsum = nboff;
+        float tsum[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) tsum[m] = nboff[m];
         if constexpr (BITS == 4) {
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             const uint32_t q = f.w[t][r][0][w];
             const uint32_t v = q >> 8;
-            tsum = dot2((q & 0x000F000Fu) | magic, xp[4 * w + 0], tsum);
-            tsum = dot2((q & 0x00F000F0u) | magic, xp[4 * w + 1], tsum);
-            tsum = dot2((v & 0x000F000Fu) | magic, xp[4 * w + 2], tsum);
-            tsum = dot2((v & 0x00F000F0u) | magic, xp[4 * w + 3], tsum);
+            const uint32_t c0 = (q & 0x000F000Fu) | magic, c1 = (q & 0x00F000F0u) | magic;
+            const uint32_t c2 = (v & 0x000F000Fu) | magic, c3 = (v & 0x00F000F0u) | magic;
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+              tsum[m] = dot2(c0, xp[m][4 * w + 0], tsum[m]);
+              tsum[m] = dot2(c1, xp[m][4 * w + 1], tsum[m]);
+              tsum[m] = dot2(c2, xp[m][4 * w + 2], tsum[m]);
+              tsum[m] = dot2(c3, xp[m][4 * w + 3], tsum[m]);
+            }
           }
         } else {
 #pragma unroll
           for (int w = 0; w < 8; ++w) {
             const uint32_t q = f.w[t][r][w >> 2][w & 3];
-            tsum = dot2(q8_lo_pair(q, magic), xp[2 * w + 0], tsum);
-            tsum = dot2(q8_hi_pair(q, magic), xp[2 * w + 1], tsum);
+            const uint32_t lo = q8_lo_pair(q, magic), hi = q8_hi_pair(q, magic);
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+              tsum[m] = dot2(lo, xp[m][2 * w + 0], tsum[m]);
+              tsum[m] = dot2(hi, xp[m][2 * w + 1], tsum[m]);
+            }
           }
         }
         const int seg = (t * R + r) * 2;
         const float sv = (float)szl[seg * SEG_STRIDE];
         const float zv = (float)szl[(seg + 1) * SEG_STRIDE];
-        acc[t * R + r] = fmaf(sv, fmaf(-zv, xs, tsum), acc[t * R + r]);
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+          acc[m * V + t * R + r] = fmaf(sv, fmaf(-zv, xsm[m], tsum[m]), acc[m * V + t * R + r]);
       }
   }
 
   // ---- 64-lane reduction (halving butterfly), then across the row group's
   // waves in LDS
-  reduce_scatter<V, 32>(acc, lane);
+  static_assert(VT <= 64 && (VT & (VT - 1)) == 0, "lane reduction shape");
+  reduce_scatter<VT, 32>(acc, lane);
   const float tot = acc[0];
   int idx = 0;
 #pragma unroll
-  for (int d = 32, h = V / 2; h >= 1; d >>= 1, h >>= 1)
+  for (int d = 32, h = VT / 2; h >= 1; d >>= 1, h >>= 1)
     if (lane & d) idx += h;
-  __shared__ float red[8][V];
-  constexpr int QUAD = 64 / V;  // lanes holding the same index
+  __shared__ float red[8][VT];
+  constexpr int QUAD = 64 / VT;  // lanes holding the same index
   if ((lane & (QUAD - 1)) == 0) red[wave][idx] = tot;
   __syncthreads();
-  if (ks != 0 || lane >= R) return;
+  if (ks != 0 || lane >= R * MR) return;
+  const int m = lane / R, rr = lane - m * R;
   float v0 = 0.0f, v1 = 0.0f;
   for (int w = 0; w < kw; ++w) {
-    v0 += red[wave + w][lane];
-    if constexpr (NMAT == 2) v1 += red[wave + w][R + lane];
+    v0 += red[wave + w][m * V + rr];
+    if constexpr (NMAT == 2) v1 += red[wave + w][m * V + R + rr];
   }
-  const int nn = n0 + lane;
-  if (nn < N) store_out<f16, EPI>(args, (size_t)nn, v0, v1);
+  const int nn = n0 + rr;
+  if (nn < N && m < args.M) store_out<f16, EPI>(args, (size_t)m * N + nn, v0, v1);
 }
 
 // --------------------------------------------------------------------------
@@ -864,7 +914,15 @@ int launch_dot(GemvArgs a, hipStream_t st) {
   const dim3 grid((unsigned)((a.N + rows - 1) / rows));
   const dim3 block((unsigned)(64 * a.kw * a.rg));
   const size_t stage_bytes = (size_t)a.kw * a.rg * NMAT * R * 2 * (2 * SEG_STRIDE);
-  gemv_dot_kernel<BITS, NMAT, EPI, NORM><<<grid, block, (NORM ? (size_t)a.K * 2 : 0) + stage_bytes, st>>>(a);
+  const size_t lds = (NORM ? (size_t)a.K * 2 : 0) + stage_bytes;
+  if constexpr (NORM) {
+    gemv_dot_kernel<BITS, NMAT, EPI, true, 1><<<grid, block, lds, st>>>(a);
+  } else {
+    if (a.M <= 1) gemv_dot_kernel<BITS, NMAT, EPI, false, 1><<<grid, block, lds, st>>>(a);
+    else if (a.M == 2) gemv_dot_kernel<BITS, NMAT, EPI, false, 2><<<grid, block, lds, st>>>(a);
+    else if constexpr (BITS == 4) gemv_dot_kernel<BITS, NMAT, EPI, false, 4><<<grid, block, lds, st>>>(a);
+    else return MK_ERR_UNSUPPORTED;  // q8: at most two rows (four would spill)
+  }
   MK_CHECK_LAUNCH();
   return MK_OK;
 }
@@ -911,14 +969,15 @@ int gemv_prepare(GemvArgs& a, int64_t N, int64_t K, int64_t gs, bool* fast) {
   return gpc;
 }
 
-// The M = 1 dot kernel: one 64-unit (2048-k) slice per wave, <= 8 waves; the
-// (s, z) runs of a slice must be whole 16-byte vectors and fit the stage.
+// The dot kernel (M <= 4): one 64-unit (2048-k) slice per wave, <= 8 waves;
+// the (s, z) runs of a slice must be whole 16-byte vectors and fit the stage.
 template <int BITS, int NMAT>
 bool dot_eligible(const GemvArgs& a, bool fast, int64_t mrows, int act_dt, int sc_dt) {
   const int lg = a.lg;
   const int64_t K = a.K;
   const int64_t gpw = lg >= 0 ? (2048 >> lg) : 0;
-  return fast && mrows == 1 && act_dt == MK_DT_F16 && sc_dt == MK_DT_F16 && lg >= 5 && lg <= 8 &&
+  return fast && mrows >= 1 && mrows <= (BITS == 4 ? 4 : 2) && act_dt == MK_DT_F16 && sc_dt == MK_DT_F16 &&
+         lg >= 5 && lg <= 8 &&
          (K % 32) == 0 && K <= 8 * 2048 && (a.G % 8) == 0 && (gpw % 8) == 0 &&
          (int64_t)NMAT * dot_rows<BITS, NMAT>() * 2 * (gpw / 8) <= 64 * DOT_SZ_VEC &&
          mk_aligned(a.s[0], 16) && mk_aligned(a.s[NMAT - 1], 16) &&
@@ -946,9 +1005,9 @@ int gemv_dispatch(GemvArgs a, int64_t M, int64_t N, int64_t K, int64_t gs, int a
   bool fast;
   const int gpc = gemv_prepare<BITS, NMAT>(a, N, K, gs, &fast);
 
-  const int64_t mblocks = (M + 15) / 16;
   const size_t xe = 2;  // activation element size
   int rc = MK_OK;
+  const int64_t mblocks = (M + 15) / 16;
   for (int64_t mb = 0; mb < mblocks && rc == MK_OK; ++mb) {
     GemvArgs b = a;
     const int64_t m0 = mb * 16;
@@ -1067,7 +1126,7 @@ int norm_gate_up_entry(const void* x, const void* residual, const void* norm_w, 
   gemv_prepare<BITS, 2>(a, N, K, gs, &fast);
   if constexpr (BITS == 4) {
     // K <= 8192: the row fits two 16-byte chunks per thread of the workgroup
-    if (nw_dt == MK_DT_F16 && K <= 4 * 2048 && dot_eligible<BITS, 2>(a, fast, M, act_dt, sc_dt) &&
+    if (nw_dt == MK_DT_F16 && K <= 4 * 2048 && M == 1 && dot_eligible<BITS, 2>(a, fast, M, act_dt, sc_dt) &&
         mk_aligned(residual, 16) &&
         mk_aligned(norm_w, 16) && mk_aligned(z_out, 16) && (!normed_out || mk_aligned(normed_out, 16))) {
       a.M = 1;
@@ -1111,7 +1170,8 @@ int norm_matvec_entry(const void* x, const void* norm_w, float eps, const uint8_
   gemv_prepare<BITS, 1>(a, N, K, gs, &fast);
   if constexpr (BITS == 4) {
     // K <= 8192: the row fits two 16-byte chunks per thread of the workgroup
-    if (nw_dt == MK_DT_F16 && K <= 4 * 2048 && dot_eligible<BITS, 1>(a, fast && mk_aligned(x, 16), M, act_dt, sc_dt) &&
+    if (nw_dt == MK_DT_F16 && K <= 4 * 2048 && M == 1 &&
+        dot_eligible<BITS, 1>(a, fast && mk_aligned(x, 16), M, act_dt, sc_dt) &&
         mk_aligned(norm_w, 16) && (!normed_out || mk_aligned(normed_out, 16))) {
       a.M = 1;
       a.kw = dot_waves(K);

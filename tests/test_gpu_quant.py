@@ -87,6 +87,94 @@ def test_matvec_f16(dev, bits, M, N, K, g):
     assert_close(got, ref, what=f"q{bits} M{M} N{N} K{K} g{g}")
 
 
+# batched decode rows (the v_dot2 kernel at M <= 4 (q8: 2), the MFMA kernel
+# above, in 16-row passes): several passes, N not a multiple of 16, group
+# 32-256, affine / absent zero points
+TILE_CASES = [
+    (2, 48, 128, 32, "sym"),
+    (5, 70, 1152, 32, "affine"),
+    (16, 100, 4096, 64, "none"),
+    (17, 40, 640, 64, "sym"),
+    (32, 48, 4096, 128, "affine"),
+    (33, 130, 640, 64, "none"),
+    (20, 16, 256, 256, "affine"),
+    (4, 3000, 14336, 64, "sym"),
+    (64, 96, 1536, 64, "sym"),
+]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M,N,K,g,zk", TILE_CASES)
+def test_batched_matvec(dev, bits, M, N, K, g, zk):
+    rng = np.random.default_rng(300 + M + N + K + g)
+    codes, stored, s, z = quant_weight(rng, N, K, g, bits, zk, "normal")
+    s = (s * 0.01).astype(np.float16).astype(np.float32)
+    xt, xf = _x(rng, M, K, "f16", dev)
+    fn = qo.q4_matvec_decode if bits == 4 else qo.q8_matvec_decode
+    got = fn(xt, to_dev(stored, dev), to_dev(s, dev, torch.float16), to_dev(z, dev, torch.float16), group_size=g)
+    mv = oq.q4_matvec if bits == 4 else oq.q8_matvec
+    ref = mv(xf.astype(np.float16), stored, s, z, g)
+    assert_close(got, ref, what=f"q{bits} M{M} N{N} K{K} g{g} {zk}")
+    # residual epilogue (the down projection's): y_mm and residual + y_mm
+    res = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float16)).to(dev)
+    ymm, out = qo.q_matvec_residual(xt, to_dev(stored, dev), to_dev(s, dev, torch.float16),
+                                    to_dev(z, dev, torch.float16), res, bits=bits, group_size=g, want_mm=True)
+    assert torch.equal(ymm, got), "same kernel, same partial sums"
+    assert_close(out, oq.residual_add(res.cpu().numpy(), ymm.cpu().numpy()), rtol=1e-3, what="residual epilogue")
+
+
+# the v_dot2 kernel with 2-4 activation rows (q8: 2; 3 runs as 4 with the
+# last row repeated): partial last 2048-k slice, N not a multiple of the
+# rows per workgroup, group 32 / 128, zeros absent
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M,N,K,g,zk", [(2, 77, 2560, 64, "sym"), (3, 130, 4096, 32, "affine"),
+                                        (4, 96, 6144, 128, "none"), (4, 4096, 14336, 64, "sym")])
+def test_dot_rows_matvec_and_gate_up(dev, bits, M, N, K, g, zk):
+    rng = np.random.default_rng(500 + M + N + K)
+    codes, stored, s, z = quant_weight(rng, N, K, g, bits, zk, "normal")
+    s = (s * 0.01).astype(np.float16).astype(np.float32)
+    xt, xf = _x(rng, M, K, "f16", dev)
+    x16 = xf.astype(np.float16)
+    mv = oq.q4_matvec if bits == 4 else oq.q8_matvec
+    fn = qo.q4_matvec_decode if bits == 4 else qo.q8_matvec_decode
+    w = (to_dev(stored, dev), to_dev(s, dev, torch.float16), to_dev(z, dev, torch.float16))
+    got = fn(xt, *w, group_size=g)
+    ref = mv(x16, stored, s, z, g)
+    assert_close(got, ref, what=f"matvec q{bits} M{M}")
+    res = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float16)).to(dev)
+    ymm, out = qo.q_matvec_residual(xt, *w, res, bits=bits, group_size=g, want_mm=True)
+    assert torch.equal(ymm, got)
+    assert_close(out, oq.residual_add(res.cpu().numpy(), ymm.cpu().numpy()), rtol=1e-3, what="residual")
+    _, su_stored, su, zu = quant_weight(rng, N, K, g, bits, zk, "normal")
+    su = (su * 0.01).astype(np.float16).astype(np.float32)
+    gfn = qo.q4_gate_up_matvec_tiled if bits == 4 else qo.q8_gate_up_matvec_tiled
+    gate, up = gfn(xt, w[0], to_dev(su_stored, dev), w[1], to_dev(su, dev, torch.float16), w[2],
+                   to_dev(zu, dev, torch.float16), group_size=g)
+    assert_close(gate, ref, what="gate")
+    assert_close(up, mv(x16, su_stored, su, zu, g), what="up")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M,N,K,g", [(4, 14336, 4096, 64), (6, 200, 1280, 64), (24, 90, 512, 32), (32, 64, 4096, 64)])
+def test_batched_gate_up(dev, bits, M, N, K, g):
+    rng = np.random.default_rng(400 + M + N)
+    _, sg_stored, sg, zg = quant_weight(rng, N, K, g, bits, "sym")
+    _, su_stored, su, zu = quant_weight(rng, N, K, g, bits, "affine", "normal")
+    su = (su * 0.01).astype(np.float16).astype(np.float32)
+    sg = sg.astype(np.float16).astype(np.float32)
+    xt, xf = _x(rng, M, K, "f16", dev)
+    args = (to_dev(sg_stored, dev), to_dev(su_stored, dev), to_dev(sg, dev, torch.float16),
+            to_dev(su, dev, torch.float16), to_dev(zg, dev, torch.float16), to_dev(zu, dev, torch.float16))
+    fn = qo.q4_gate_up_matvec_tiled if bits == 4 else qo.q8_gate_up_matvec_tiled
+    gate, up = fn(xt, *args, group_size=g)
+    mv = oq.q4_matvec if bits == 4 else oq.q8_matvec
+    x16 = xf.astype(np.float16)
+    assert_close(gate, mv(x16, sg_stored, sg, zg, g), what="gate")
+    assert_close(up, mv(x16, su_stored, su, zu, g), what="up")
+    mlp_out = qo.q_gate_up_swiglu(xt, *args, bits=bits, group_size=g)
+    assert_close(mlp_out, oq.swiglu(gate.cpu().numpy(), up.cpu().numpy()), rtol=1e-3, what="swiglu epilogue")
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("act", ["f16", "bf16"])
 @pytest.mark.parametrize("zeros_kind", ["none", "affine"])
