@@ -7,8 +7,8 @@
 // hardware a 32-bit word holds 8 consecutive codes, nibble i at bits 4i.
 //
 // Decode batches of at most 4 rows (q8: 2) with fp16 activations and scales
-// take the v_dot2 kernel below; larger batches, bf16 and fp32 scales the
-// MFMA path:
+// take the v_dot2 kernel below, 17-32 rows the two-column-tile kernel;
+// the rest, bf16 and fp32 scales the MFMA path:
 // Fast path (M <= 16 per launch, K % 64 == 0 for q4 / % 32 for q8, power-of-two
 // group size >= 16 (q4) / >= 8 (q8)):
 //   * one workgroup owns a 16-row output tile; its KW waves split K;
@@ -394,6 +394,174 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(const GemvArgs args) {
     const int nn = nb + i;
     if (nn >= N) break;
     store_out<AT, EPI>(args, (size_t)m * N + nn, acc[0][i], acc[NMAT - 1][i]);
+  }
+}
+
+// --------------------------------------------------------------------------
+// Batched decode tile kernel: fp16 activations and fp16 scales, M <= 16 * MT
+// rows per launch, power-of-two group size >= 32, K % 128 == 0.  Used with
+// MT = 2 for 17-32 rows (a batch-32 decode step): one pass over the weights
+// instead of two 16-row MFMA passes.
+//
+// A workgroup owns 16 output rows of NMAT matrices; its kw waves split K
+// into 128-k chunks.  Per chunk, lane (r = l % 16, kb = l / 16) takes the 32
+// consecutive k at 32 * kb: 16 code bytes (q4) or 32 (q8) of row r, the
+// (s, z) of the one group they lie in, and x over the same k for column r of
+// each of the MT activation tiles -- four v_mfma_f32_16x16x32_f16 steps, the
+// dequantized weight operand shared by the MT column tiles.
+// The loads run NB chunks ahead in a ring of register buffers refilled in
+// place (the loop is unrolled by NB, so no buffer is copied and every buffer
+// keeps its registers): a chunk's x, codes and scales were issued NB - 1
+// chunks before it is computed, and vmcnt retires in issue order, so computing
+// a chunk waits for its own loads only.  Columns past M read row M - 1 (their
+// results are dropped); the chunks past a wave's range in its last ring
+// re-read its first chunk and are computed with x and s zeroed.
+// --------------------------------------------------------------------------
+template <int BITS, int NMAT, int MT>
+struct TileBuf {
+  u32x4 x[MT][4];                     // 4 steps x 8 halves per column tile
+  u32x4 w[NMAT][BITS == 4 ? 1 : 2];   // 16 / 32 code bytes
+  f16 s[NMAT];
+  f16 z[NMAT];
+  bool live;
+};
+
+template <int BITS, int NMAT, int MT, int NB, int EPI>
+__global__ __launch_bounds__(NMAT == 1 && BITS == 4 ? 1024 : 512) void gemv_tile_kernel(const GemvArgs args) {
+  constexpr int WB = BITS == 4 ? 1 : 2;  // 16-byte code vectors per lane per chunk
+  constexpr int CB = 16 * WB;            // code bytes per lane per chunk
+  using Buf = TileBuf<BITS, NMAT, MT>;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loop control
+  const int kw = args.kw;
+  const int M = args.M, N = args.N, K = args.K;
+  const int n0 = blockIdx.x * 16;
+  const int r = lane & 15;
+  const int kb = lane >> 4;
+  const int n_ld = n0 + r < N ? n0 + r : N - 1;  // rows past N load a valid row; results dropped
+  const uint32_t magic = in_vgpr(BITS == 4 ? 0x64006400u : 0x64646464u);
+  const bool has_z = args.z[0] != nullptr;
+
+  const int chunks = K >> 7;
+  const int c_begin = (chunks * wave) / kw;
+  const int c_end = (chunks * (wave + 1)) / kw;
+
+  const uint8_t* wrow[NMAT];
+  const f16* srow[NMAT];
+  const f16* zrow[NMAT];
+#pragma unroll
+  for (int t = 0; t < NMAT; ++t) {
+    wrow[t] = args.w[t] + (size_t)n_ld * args.row_bytes + kb * CB;
+    srow[t] = reinterpret_cast<const f16*>(args.s[t]) + (size_t)n_ld * args.G;
+    zrow[t] = has_z ? reinterpret_cast<const f16*>(args.z[t]) + (size_t)n_ld * args.G : srow[t];
+  }
+  const f16* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + r;
+    xrow[mt] = reinterpret_cast<const f16*>(args.x) + (size_t)(m < M ? m : M - 1) * K + 32 * kb;
+  }
+
+  // x first, then the codes and scales: the order the chunk is consumed in
+  auto issue = [&](int c, Buf& b) {
+    b.live = c < c_end;
+    const int cc = b.live ? c : c_begin;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) b.x[mt][s] = ldg128(xrow[mt] + cc * 128 + 8 * s);
+    const int g = (cc * 128 + 32 * kb) >> args.lg;
+#pragma unroll
+    for (int t = 0; t < NMAT; ++t) {
+      const uint8_t* p = wrow[t] + (size_t)cc * (4 * CB);
+#pragma unroll
+      for (int v = 0; v < WB; ++v) b.w[t][v] = ldg128_stream(p + 16 * v);
+      b.s[t] = srow[t][g];
+      b.z[t] = zrow[t][g];
+    }
+  };
+
+  f32x4 acc[NMAT][MT];
+#pragma unroll
+  for (int t = 0; t < NMAT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const Buf& b, auto masked) {
+    constexpr bool MASKED = decltype(masked)::value;
+    u32x4 xp[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        xp[mt][s] = xperm<BITS, true>(b.x[mt][s]);
+        if constexpr (MASKED)
+          if (!b.live) xp[mt][s] = (u32x4){0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+    for (int t = 0; t < NMAT; ++t) {
+      f16 sc = b.s[t];
+      if constexpr (MASKED)
+        if (!b.live) sc = (f16)0.0f;
+      const GpMagic gp = make_gp_magic(sc, has_z ? b.z[t] : (f16)0.0f);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        u32x4 a;
+        if constexpr (BITS == 4) a = dq4_magic(b.w[t][0][s], gp, magic);
+        else a = dq8_magic(b.w[t][s >> 1][(2 * s) & 3], b.w[t][s >> 1][(2 * s + 1) & 3], gp, magic);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mfma_k32<f16>(a, xp[mt][s], acc[t][mt]);
+      }
+    }
+  };
+
+  // scheduling barriers keep each buffer's loads together and in ring order,
+  // so the wait before a chunk's compute leaves NB - 1 buffers in flight
+  Buf b[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    issue(c_begin + i, b[i]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  int c = c_begin;
+  for (; c + NB < c_end; c += NB) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      compute(b[i], std::false_type{});
+      __builtin_amdgcn_sched_barrier(0);
+      issue(c + NB + i, b[i]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i) compute(b[i], std::true_type{});
+
+  // ---- cross-wave reduction through LDS: [kw][NMAT * MT][64] partial tiles
+  extern __shared__ __align__(16) uint8_t tile_red_raw[];
+  f32x4* red = reinterpret_cast<f32x4*>(tile_red_raw);
+#pragma unroll
+  for (int t = 0; t < NMAT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) red[(wave * NMAT * MT + t * MT + mt) * 64 + lane] = acc[t][mt];
+  __syncthreads();
+  // wave j finishes column tile j (j < MT): lane holds D[n = 4 kb + i][m = 16 j + r]
+  if (wave >= MT) return;
+  const int mt = wave;
+  const int m = 16 * mt + r;
+  f32x4 v[NMAT];
+#pragma unroll
+  for (int t = 0; t < NMAT; ++t) {
+    v[t] = red[(t * MT + mt) * 64 + lane];
+    for (int w = 1; w < kw; ++w) v[t] += red[(w * NMAT * MT + t * MT + mt) * 64 + lane];
+  }
+  if (m >= M) return;
+  const int nb = n0 + 4 * kb;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int nn = nb + i;
+    if (nn >= N) break;
+    store_out<f16, EPI>(args, (size_t)m * N + nn, v[0][i], v[NMAT - 1][i]);
   }
 }
 
@@ -899,6 +1067,46 @@ int launch_fast(const GemvArgs& a, int gpc, hipStream_t st) {
   return MK_OK;
 }
 
+// Tile kernel plan: ring depth NB (4 chunks for q4 at one column tile; 2
+// where the x or q8 code registers double) and kw waves per 16-row tile,
+// kw <= 16 for a single q4 matrix, else 8 (1024 / 512 threads), preferring a
+// split that gives every wave a whole number of rings and at least one.
+template <int BITS, int MT>
+constexpr int tile_ring() { return BITS == 4 && MT == 1 ? 4 : 2; }
+
+template <int BITS, int NMAT>
+inline int tile_choose_kw(int64_t K, int nb) {
+  const int64_t chunks = K / 128;
+  const int kmax = NMAT == 1 && BITS == 4 ? 16 : 8;
+  for (int kw = kmax; kw >= 1; --kw)
+    if (chunks % kw == 0 && (chunks / kw) % nb == 0) return kw;
+  int64_t kw = (chunks + nb - 1) / nb;  // every wave at least one ring
+  return (int)(kw < 1 ? 1 : (kw > kmax ? kmax : kw));
+}
+
+template <int BITS, int NMAT, int MT, int EPI>
+int launch_tile(GemvArgs a, hipStream_t st) {
+  constexpr int NB = tile_ring<BITS, MT>();
+  a.kw = tile_choose_kw<BITS, NMAT>(a.K, NB);
+  if (a.kw < MT) a.kw = MT;  // wave j finishes column tile j
+  const dim3 grid((unsigned)((a.N + 15) / 16));
+  const dim3 block((unsigned)(64 * a.kw));
+  const size_t lds = (size_t)a.kw * NMAT * MT * 64 * sizeof(f32x4);
+  gemv_tile_kernel<BITS, NMAT, MT, NB, EPI><<<grid, block, lds, st>>>(a);
+  MK_CHECK_LAUNCH();
+  return MK_OK;
+}
+
+// fp16 activations and scales, power-of-two group >= 32, K % 128 == 0, 16-byte
+// aligned x and codes
+template <int NMAT>
+bool tile_eligible(const GemvArgs& a, int act_dt, int sc_dt) {
+  bool ok = act_dt == MK_DT_F16 && sc_dt == MK_DT_F16 && a.lg >= 5 && (a.K % 128) == 0 &&
+            mk_aligned(a.x, 16) && (size_t)a.row_bytes % 16 == 0;
+  for (int t = 0; t < NMAT; ++t) ok = ok && mk_aligned(a.w[t], 16);
+  return ok;
+}
+
 // Row groups per dot workgroup: one for the plain kernel (measured: sharing
 // x through LDS costs a barrier that outweighs its L2 savings); two for the
 // norm prologue (four at K <= 2048), which keeps K / 8 <= 2 * blockDim.x for
@@ -1007,10 +1215,26 @@ int gemv_dispatch(GemvArgs a, int64_t M, int64_t N, int64_t K, int64_t gs, int a
 
   const size_t xe = 2;  // activation element size
   int rc = MK_OK;
-  const int64_t mblocks = (M + 15) / 16;
+  // 17-32 rows at a time through the two-column-tile kernel, the rest below
+  int64_t m_done = 0;
+  if (tile_eligible<NMAT>(a, act_dt, sc_dt)) {
+    while (M - m_done >= 17 && rc == MK_OK) {
+      GemvArgs b = a;
+      const int64_t mrows = (M - m_done) < 32 ? (M - m_done) : 32;
+      b.M = (int)mrows;
+      b.x = (const char*)a.x + (size_t)m_done * K * xe;
+      if (a.residual) b.residual = (const char*)a.residual + (size_t)m_done * N * xe;
+      if (a.y0) b.y0 = (char*)a.y0 + (size_t)m_done * N * xe;
+      if (a.y1) b.y1 = (char*)a.y1 + (size_t)m_done * N * xe;
+      if (a.y2) b.y2 = (char*)a.y2 + (size_t)m_done * N * xe;
+      rc = launch_tile<BITS, NMAT, 2, EPI>(b, st);
+      m_done += mrows;
+    }
+  }
+  const int64_t mblocks = (M - m_done + 15) / 16;
   for (int64_t mb = 0; mb < mblocks && rc == MK_OK; ++mb) {
     GemvArgs b = a;
-    const int64_t m0 = mb * 16;
+    const int64_t m0 = m_done + mb * 16;
     const int64_t mrows = (M - m0) < 16 ? (M - m0) : 16;
     b.M = (int)mrows;
     b.x = (const char*)a.x + (size_t)m0 * K * xe;
