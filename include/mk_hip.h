@@ -145,6 +145,34 @@ int mk_q8_rmsnorm_matvec(const void* x, const void* norm_w, float eps, const uin
                          const void* zeros, void* normed_out, void* y, int64_t M, int64_t N, int64_t K,
                          int64_t group_size, int act_dtype, int scale_dtype, int norm_w_dtype, void* stream);
 
+/* A decode layer's front half up to attention, in one launch where it can:
+ * RMSNorm (ops/llama_layer_ops.py:256-258) + qkv projection
+ * (ops/quantized_decode_block_ops.py:154-184) + GQA split + interleaved RoPE
+ * + paged K/V write of the new token (ops/gqa_ops.py:493-547, as
+ * mk_qkv_rope_paged_update).  x [M, K]; w [(Hq + 2 Hkv) D, K] packed; the
+ * rounding of every stage is that of mk_q*_rmsnorm_matvec followed by
+ * mk_qkv_rope_paged_update, so q_out and the caches match that pair exactly.
+ * One launch for q4 fp16 (activations, scales, norm weight, pages) with
+ * M == 1 and K <= 8192, where qkv_scratch is not written and normed_out may
+ * be NULL; otherwise the pair runs, projecting through qkv_scratch [M, (Hq +
+ * 2 Hkv) D] and normed_out [M, K] (then required).  K/V pages carry the
+ * activation dtype. */
+int mk_q4_rmsnorm_qkv_rope_paged(const void* x, const void* norm_w, float eps, const uint8_t* w, const void* scales,
+                                 const void* zeros, void* qkv_scratch, void* normed_out, const float* cos_t,
+                                 const float* sin_t, const int32_t* positions, const int32_t* block_table,
+                                 void* K_pages, void* V_pages, void* q_out, int64_t M, int64_t Hq, int64_t Hkv,
+                                 int64_t D, int64_t page_size, int64_t max_blocks, int64_t num_pages,
+                                 int64_t cos_rows, int64_t K, int64_t group_size, int act_dtype, int scale_dtype,
+                                 int norm_w_dtype, void* stream);
+
+int mk_q8_rmsnorm_qkv_rope_paged(const void* x, const void* norm_w, float eps, const uint8_t* w, const void* scales,
+                                 const void* zeros, void* qkv_scratch, void* normed_out, const float* cos_t,
+                                 const float* sin_t, const int32_t* positions, const int32_t* block_table,
+                                 void* K_pages, void* V_pages, void* q_out, int64_t M, int64_t Hq, int64_t Hkv,
+                                 int64_t D, int64_t page_size, int64_t max_blocks, int64_t num_pages,
+                                 int64_t cos_rows, int64_t K, int64_t group_size, int act_dtype, int scale_dtype,
+                                 int norm_w_dtype, void* stream);
+
 /* ---------------------------------------------------------------- elementwise / norm */
 
 /* greedy_sample -- models/sampling.py:120-124 (np.argmax per row): out[r] = the

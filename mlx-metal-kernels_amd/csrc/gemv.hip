@@ -26,12 +26,14 @@
 // The MFMA contraction is order-free in k, so the activation operand is built
 // in the same permuted k order the magic unpack produces.
 #include "common.h"
+#include "paged_common.h"
 
 namespace {
 
 constexpr int EPI_NONE = 0;
 constexpr int EPI_RESIDUAL = 1;
 constexpr int EPI_GATE_UP = 2;
+constexpr int EPI_ROPE_KV = 3;  // qkv rows -> split + interleaved RoPE + paged K/V write
 
 template <int BITS>
 struct QFmt {
@@ -198,6 +200,19 @@ __device__ __forceinline__ float ld_scalar_f32(const ST* p) {
   return to_f32(*p);
 }
 
+// The decode token's cache write fused into the qkv projection's epilogue
+// (EPI_ROPE_KV): the operands of qkv_rope_update_kernel.
+struct RopeKV {
+  const float* cos_t;   // [cos_rows, D/2]
+  const float* sin_t;
+  const int32_t* pos;   // [M]
+  const int32_t* bt;    // [M, max_blocks]
+  void* kp;             // [num_pages, P, Hkv, D] f16
+  void* vp;
+  void* q_out;          // [M, Hq, D] f16
+  int Hq, Hkv, D, P, max_blocks, num_pages, cos_rows;
+};
+
 struct GemvArgs {
   const void* x;         // [M, K]
   const uint8_t* w[2];   // [N, row_bytes]
@@ -222,6 +237,7 @@ struct GemvArgs {
   void* zout;            // [K]
   void* nout;            // [K] or null
   float eps;
+  RopeKV rk;             // EPI_ROPE_KV only
 };
 
 // --------------------------------------------------------------------------
@@ -247,6 +263,46 @@ __device__ __forceinline__ void store_out(const GemvArgs& args, size_t o, float 
       reinterpret_cast<AT*>(args.y2)[o] = from_f32<AT>(sil * to_f32(u));
     }
   }
+}
+
+// EPI_ROPE_KV: qkv output n of row m, rounded as the projection stores it,
+// then the arithmetic of qkv_rope_update_kernel -- q and k pairs (n, n ^ 1)
+// rotated in fp32 and rounded, v copied; q to q_out, k and v to the token's
+// cache slot unless its position is out of range or a later row takes the
+// slot.  Called by every lane of the pair (the partner value comes by
+// shuffle), whether or not (m, n) is in range.
+__device__ __forceinline__ void rope_kv_store(const GemvArgs& a, int m, int n, float v) {
+  const f16 hv = saturate_cast<f16>(v);
+  const float xv = to_f32(hv);
+  const float xo = __shfl_xor(xv, 1, 64);
+  if (n >= a.N || m >= a.M) return;
+  const RopeKV& r = a.rk;
+  const int p = r.pos[m];
+  if (p < 0 || p >= r.cos_rows) return;
+  const int D = r.D, QD = r.Hq * D, KD = r.Hkv * D;
+  const int d = n % D;
+  f16 out = hv;
+  f16* dst = reinterpret_cast<f16*>(r.vp);
+  int h;
+  if (n < QD + KD) {
+    const bool even = (d & 1) == 0;
+    const size_t ci = (size_t)p * (D / 2) + (d >> 1);
+    float ye, yo;
+    rope_pair(even ? xv : xo, even ? xo : xv, r.cos_t[ci], r.sin_t[ci], &ye, &yo);
+    out = from_f32<f16>(even ? ye : yo);
+    if (n < QD) {
+      reinterpret_cast<f16*>(r.q_out)[(size_t)m * QD + n] = out;
+      return;
+    }
+    dst = reinterpret_cast<f16*>(r.kp);
+    h = (n - QD) / D;
+  } else {
+    h = (n - QD - KD) / D;
+  }
+  int off;
+  const int page = slot_page(r.bt, r.pos, m, r.max_blocks, r.P, r.num_pages, &off);
+  if (page < 0 || superseded(r.bt, r.pos, m, a.M, r.max_blocks, r.P, r.num_pages, page, off)) return;
+  dst[((size_t)page * r.P + off) * KD + (size_t)h * D + d] = out;
 }
 
 // --------------------------------------------------------------------------
@@ -980,6 +1036,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     if constexpr (NMAT == 2) v1 += red[wave + w][m * V + R + rr];
   }
   const int nn = n0 + rr;
+  if constexpr (EPI == EPI_ROPE_KV) {
+    rope_kv_store(args, m, nn, v0);  // lane pairs (rr even, rr + 1) never straddle a head: R and D even
+    return;
+  }
   if (nn < N && m < args.M) store_out<f16, EPI>(args, (size_t)m * N + nn, v0, v1);
 }
 
@@ -1413,9 +1473,82 @@ int norm_matvec_entry(const void* x, const void* norm_w, float eps, const uint8_
   return matvec_entry<BITS>(normed_out, w, s, z, nullptr, nullptr, y, M, N, K, gs, act_dt, sc_dt, stream);
 }
 
+// RMSNorm + qkv projection + split + RoPE + paged K/V write.  One launch
+// (the NORM dot kernel with the EPI_ROPE_KV epilogue) for a q4 fp16 row with
+// K <= 8192; otherwise the projection into qkv_scratch, then
+// mk_qkv_rope_paged_update.
+template <int BITS>
+int norm_qkv_rope_entry(const void* x, const void* norm_w, float eps, const uint8_t* w, const void* s,
+                        const void* z, void* qkv_scratch, void* normed_out, const float* cos_t,
+                        const float* sin_t, const int32_t* positions, const int32_t* block_table, void* K_pages,
+                        void* V_pages, void* q_out, int64_t M, int64_t Hq, int64_t Hkv, int64_t D, int64_t P,
+                        int64_t max_blocks, int64_t num_pages, int64_t cos_rows, int64_t K, int64_t gs,
+                        int act_dt, int sc_dt, int nw_dt, void* stream) {
+  MK_REQUIRE(x && norm_w && w && s && qkv_scratch && cos_t && sin_t && positions && block_table && K_pages &&
+             V_pages && q_out);
+  MK_REQUIRE(M >= 0 && M < 65536 && Hq > 0 && Hkv > 0 && D > 0 && (D % 2) == 0 && P > 0 && max_blocks > 0 &&
+             num_pages > 0 && cos_rows > 0 && K > 0 && gs > 0);
+  MK_REQUIRE((Hq + 2 * Hkv) * D < (1LL << 31) && num_pages < (1LL << 31) && max_blocks * P < (1LL << 31));
+  MK_REQUIRE(act_dt == MK_DT_F16 || act_dt == MK_DT_BF16);
+  if (M == 0) return MK_OK;
+  const int64_t N = (Hq + 2 * Hkv) * D;
+  if constexpr (BITS == 4) {
+    GemvArgs a = {};
+    a.x = x;
+    a.w[0] = a.w[1] = w;
+    a.s[0] = a.s[1] = s;
+    a.z[0] = a.z[1] = z;
+    bool fast;
+    gemv_prepare<BITS, 1>(a, N, K, gs, &fast);
+    if (act_dt == MK_DT_F16 && sc_dt == MK_DT_F16 && nw_dt == MK_DT_F16 && K <= 4 * 2048 && M == 1 &&
+        dot_eligible<BITS, 1>(a, fast && mk_aligned(x, 16), M, act_dt, sc_dt) && mk_aligned(norm_w, 16) &&
+        (!normed_out || mk_aligned(normed_out, 16))) {
+      a.M = 1;
+      a.kw = dot_waves(K);
+      a.nres = nullptr;
+      a.nw = norm_w;
+      a.zout = nullptr;
+      a.nout = normed_out;
+      a.eps = eps;
+      a.rk = RopeKV{cos_t, sin_t, positions, block_table, K_pages, V_pages, q_out, (int)Hq, (int)Hkv, (int)D,
+                    (int)P, (int)max_blocks, (int)num_pages, (int)cos_rows};
+      return launch_dot<BITS, 1, EPI_ROPE_KV, true>(a, reinterpret_cast<hipStream_t>(stream));
+    }
+  }
+  const int rc = norm_matvec_entry<BITS>(x, norm_w, eps, w, s, z, normed_out, qkv_scratch, M, N, K, gs, act_dt,
+                                         sc_dt, nw_dt, stream);
+  if (rc != MK_OK) return rc;
+  return mk_qkv_rope_paged_update(qkv_scratch, cos_t, sin_t, positions, block_table, K_pages, V_pages, q_out, M, Hq,
+                                  Hkv, D, P, max_blocks, num_pages, cos_rows, act_dt, stream);
+}
+
 }  // namespace
 
 extern "C" {
+
+int mk_q4_rmsnorm_qkv_rope_paged(const void* x, const void* norm_w, float eps, const uint8_t* w, const void* scales,
+                                 const void* zeros, void* qkv_scratch, void* normed_out, const float* cos_t,
+                                 const float* sin_t, const int32_t* positions, const int32_t* block_table,
+                                 void* K_pages, void* V_pages, void* q_out, int64_t M, int64_t Hq, int64_t Hkv,
+                                 int64_t D, int64_t page_size, int64_t max_blocks, int64_t num_pages,
+                                 int64_t cos_rows, int64_t K, int64_t group_size, int act_dtype, int scale_dtype,
+                                 int norm_w_dtype, void* stream) {
+  return norm_qkv_rope_entry<4>(x, norm_w, eps, w, scales, zeros, qkv_scratch, normed_out, cos_t, sin_t, positions,
+                                block_table, K_pages, V_pages, q_out, M, Hq, Hkv, D, page_size, max_blocks,
+                                num_pages, cos_rows, K, group_size, act_dtype, scale_dtype, norm_w_dtype, stream);
+}
+
+int mk_q8_rmsnorm_qkv_rope_paged(const void* x, const void* norm_w, float eps, const uint8_t* w, const void* scales,
+                                 const void* zeros, void* qkv_scratch, void* normed_out, const float* cos_t,
+                                 const float* sin_t, const int32_t* positions, const int32_t* block_table,
+                                 void* K_pages, void* V_pages, void* q_out, int64_t M, int64_t Hq, int64_t Hkv,
+                                 int64_t D, int64_t page_size, int64_t max_blocks, int64_t num_pages,
+                                 int64_t cos_rows, int64_t K, int64_t group_size, int act_dtype, int scale_dtype,
+                                 int norm_w_dtype, void* stream) {
+  return norm_qkv_rope_entry<8>(x, norm_w, eps, w, scales, zeros, qkv_scratch, normed_out, cos_t, sin_t, positions,
+                                block_table, K_pages, V_pages, q_out, M, Hq, Hkv, D, page_size, max_blocks,
+                                num_pages, cos_rows, K, group_size, act_dtype, scale_dtype, norm_w_dtype, stream);
+}
 
 int mk_q4_rmsnorm_matvec(const void* x, const void* norm_w, float eps, const uint8_t* w, const void* scales,
                          const void* zeros, void* normed_out, void* y, int64_t M, int64_t N, int64_t K,

@@ -13,30 +13,9 @@
 // as the reference's loop over b does: a sequence skips its cache write when a
 // later sequence targets the same (page, offset).
 #include "common.h"
+#include "paged_common.h"
 
 namespace {
-
-__device__ __forceinline__ int slot_page(const int32_t* bt, const int32_t* pos, int b,
-                                         int max_blocks, int P, int num_pages, int* off) {
-  const int p = pos[b];
-  if (p < 0 || p >= max_blocks * P) return -1;
-  const int page = bt[(size_t)b * max_blocks + p / P];
-  *off = p % P;
-  if (page < 0 || page >= num_pages) return -1;
-  return page;
-}
-
-// true when a later sequence writes the same slot (its write must win)
-__device__ __forceinline__ bool superseded(const int32_t* bt, const int32_t* pos, int b, int B,
-                                           int max_blocks, int P, int num_pages, int page,
-                                           int off) {
-  for (int b2 = b + 1; b2 < B; ++b2) {
-    int o2;
-    const int p2 = slot_page(bt, pos, b2, max_blocks, P, num_pages, &o2);
-    if (p2 == page && o2 == off) return true;
-  }
-  return false;
-}
 
 __global__ void block_table_lookup_kernel(const int32_t* __restrict__ bt,
                                           const int32_t* __restrict__ pos, int32_t* page_ids,
@@ -67,19 +46,6 @@ __global__ void paged_update_kernel(T* __restrict__ Kp, T* __restrict__ Vp,
     Kp[dst + i] = k[src + i];
     Vp[dst + i] = v[src + i];
   }
-}
-
-// interleaved RoPE of one (even, odd) pair; products and sums rounded
-// separately (no fma contraction), matching the reference's fp32 expression
-__device__ __forceinline__ void rope_pair(float xe, float xo, float c, float s, float* ye,
-                                          float* yo) {
-#pragma clang fp contract(off)
-  const float a = xe * c;
-  const float b2 = xo * s;
-  const float d = xe * s;
-  const float e = xo * c;
-  *ye = a - b2;
-  *yo = d + e;
 }
 
 // qkv row layout: [Q (Hq*D) | K (Hkv*D) | V (Hkv*D)]

@@ -54,6 +54,8 @@ SIGNATURES: dict[str, list] = {
     "mk_q4_gate_up": [_P] * 10 + [_I64] * 4 + [_I, _I, _P],
     "mk_q8_gate_up": [_P] * 10 + [_I64] * 4 + [_I, _I, _P],
     "mk_argmax_rows": [_P, _P, _I64, _I64, _I, _P],
+    "mk_q4_rmsnorm_qkv_rope_paged": [_P, _P, _F] + [_P] * 12 + [_I64] * 10 + [_I, _I, _I, _P],
+    "mk_q8_rmsnorm_qkv_rope_paged": [_P, _P, _F] + [_P] * 12 + [_I64] * 10 + [_I, _I, _I, _P],
     "mk_q4_rmsnorm_matvec": [_P, _P, _F] + [_P] * 5 + [_I64] * 4 + [_I, _I, _I, _P],
     "mk_q8_rmsnorm_matvec": [_P, _P, _F] + [_P] * 5 + [_I64] * 4 + [_I, _I, _I, _P],
     "mk_q4_rmsnorm_gate_up": [_P, _P, _P, _F] + [_P] * 11 + [_I64] * 4 + [_I, _I, _I, _P],

@@ -188,12 +188,16 @@ def llama_layer_decode_step(x, weights: LlamaLayerKernelWeights, cache, cos, sin
     config = config.validate()
     weights.validate(config)
     K_pages, V_pages, block_table = _check_decode(x, config, cache, cache_layout)
-    h, K_pages, V_pages, qkv, attn_out = paged_quantized_decode_block(
+    # without intermediates the norm, qkv projection, RoPE and cache write are
+    # one launch (the projection is then never materialised)
+    blk = paged_quantized_decode_block(
         x, weights.qkv_w, weights.qkv_scales, weights.o_w, weights.o_scales, K_pages, V_pages, block_table, cos,
         sin, position, qkv_zeros=weights.qkv_zeros, out_zeros=weights.o_zeros, bits=weights.bits,
         group_size=weights.group_size, H=config.num_attention_heads, num_key_value_heads=config.num_key_value_heads,
-        head_dim=config.head_dim, return_intermediates=True, residual=x,
+        head_dim=config.head_dim, return_intermediates=return_intermediates, residual=x,
         norm_weight=weights.input_layernorm_weight, eps=config.rms_norm_eps, lengths=lengths)
+    h, K_pages, V_pages = blk[:3]
+    qkv, attn_out = (blk[3], blk[4]) if return_intermediates else (None, None)
     res = quantized_mlp_block(h, _zero_residual(h), weights.post_attention_layernorm_weight, weights.gate_w,
                               weights.gate_scales, weights.up_w, weights.up_scales, weights.down_w, weights.down_scales,
                               gate_zeros=weights.gate_zeros, up_zeros=weights.up_zeros, down_zeros=weights.down_zeros,

@@ -16,8 +16,14 @@ from __future__ import annotations
 
 import math
 
+import torch
+
+from . import _lib
+from ._common import as_u8, scales_for_kernel
 from .gqa_ops import paged_gqa_decode_block_from_qkv, reference_paged_gqa_decode_block_from_qkv
+from .kv_cache_ops import normalize_positions
 from .norm_ops import reference_rms_norm
+from .paged_kv_ops import _hip_paged_attention, _i32
 from .quant_ops import (
     q4_matvec_decode,
     q8_matvec_decode,
@@ -166,6 +172,59 @@ def _block_dims(qkv_w, H, num_key_value_heads, head_dim, D, bits):
     return H, kv_heads, D
 
 
+def rmsnorm_qkv_rope_paged_update(x2d, norm_weight, qkv_w, qkv_scales, qkv_zeros, K_pages, V_pages, block_table,
+                                  cos, sin, position, *, num_attention_heads, num_key_value_heads, head_dim, bits=4,
+                                  group_size=32, eps=1e-5):
+    """Input RMSNorm + qkv projection + GQA split + interleaved RoPE + paged
+    write of the new token (ops/llama_layer_ops.py:256-260 feeding
+    ops/gqa_ops.py:493-547 up to the attention call) -- one HIP launch for a
+    q4 fp16 decode row (mk_q4_rmsnorm_qkv_rope_paged), the projection then
+    mk_qkv_rope_paged_update otherwise, with identical rounding either way.
+    x2d [B, hidden]; K_pages/V_pages [NUM_PAGES, P, Hkv, D] in x's dtype,
+    updated in place.  Returns (q [B, 1, Hq, D], positions int32 [B])."""
+    Hq, Hkv, D = num_attention_heads, num_key_value_heads, head_dim
+    if bits not in (4, 8):
+        raise ValueError(f"bits must be 4 or 8, got {bits}")
+    if D % 2 != 0:
+        raise ValueError(f"RoPE requires even D, got D={D}")
+    if K_pages.shape != V_pages.shape or K_pages.ndim != 4 or K_pages.shape[2] != Hkv or K_pages.shape[3] != D:
+        raise ValueError(f"K_pages/V_pages must be [NUM_PAGES,PAGE_SIZE,{Hkv},{D}], got {tuple(K_pages.shape)}")
+    if K_pages.dtype != x2d.dtype or V_pages.dtype != x2d.dtype:
+        raise TypeError(f"K_pages/V_pages must carry the activation dtype {x2d.dtype}")
+    if not (K_pages.is_contiguous() and V_pages.is_contiguous()):
+        raise ValueError("K_pages and V_pages must be contiguous for the in-place update")
+    B, K = x2d.shape
+    if tuple(norm_weight.shape) != (K,):
+        raise ValueError(f"norm_weight must have shape {(K,)}, got {tuple(norm_weight.shape)}")
+    if block_table.shape[0] != B:
+        raise ValueError(f"block_table batch {block_table.shape[0]} != x batch {B}")
+    N = (Hq + 2 * Hkv) * D
+    w8 = as_u8(qkv_w)
+    cols = math.ceil(K / 2) if bits == 4 else K
+    if w8.ndim != 2 or tuple(w8.shape) != (N, cols):
+        raise ValueError(f"qkv_w must have shape [{N},{cols}], got {tuple(w8.shape)}")
+    x2d = x2d.contiguous()
+    nw = norm_weight.contiguous()
+    dev = _lib.require_device(x2d, nw, w8, qkv_scales, qkv_zeros, K_pages, V_pages, block_table)
+    s, z = scales_for_kernel(qkv_scales, qkv_zeros)
+    P, MAX_BLOCKS = K_pages.shape[1], block_table.shape[1]
+    pos = normalize_positions(position, B, cos.shape[0], device=dev)
+    pos = normalize_positions(pos, B, MAX_BLOCKS * P, device=dev)
+    c = cos.to(device=dev, dtype=torch.float32).contiguous()
+    sn = sin.to(device=dev, dtype=torch.float32).contiguous()
+    bt = _i32(block_table, dev)
+    q_out = torch.empty((B, 1, Hq, D), dtype=x2d.dtype, device=dev)
+    scratch = torch.empty((B, N), dtype=x2d.dtype, device=dev)  # the two-launch path's projection
+    normed = torch.empty_like(x2d)
+    name = "mk_q4_rmsnorm_qkv_rope_paged" if bits == 4 else "mk_q8_rmsnorm_qkv_rope_paged"
+    _lib.launch(name, dev, _lib.ptr(x2d), _lib.ptr(nw), float(eps), _lib.ptr(w8), _lib.ptr(s), _lib.ptr(z),
+                _lib.ptr(scratch), _lib.ptr(normed), _lib.ptr(c), _lib.ptr(sn), _lib.ptr(pos), _lib.ptr(bt),
+                _lib.ptr(K_pages), _lib.ptr(V_pages), _lib.ptr(q_out), B, Hq, Hkv, D, P, MAX_BLOCKS,
+                K_pages.shape[0], c.shape[0], K, group_size, _lib.dtype_code(x2d.dtype), _lib.dtype_code(s.dtype),
+                _lib.dtype_code(nw.dtype))
+    return q_out, pos
+
+
 def paged_quantized_decode_block(x, qkv_w, qkv_scales, out_w, out_scales, K_pages, V_pages, block_table, cos, sin,
                                  position, *, qkv_zeros=None, out_zeros=None, bits=4, group_size=32, H=None,
                                  num_key_value_heads=None, head_dim=None, D=None, scale=None,
@@ -189,7 +248,19 @@ def paged_quantized_decode_block(x, qkv_w, qkv_scales, out_w, out_scales, K_page
     validate_quantized_weight_shapes(x2d.new_empty((x2d.shape[0], H * D)), out_w, out_scales, out_zeros, bits=bits,
                                      group_size=group_size, expected_in_dim=H * D, name="output_projection")
     reference = matvec_backend.lower() == "reference"
-    if norm_weight is not None and not reference:
+    fuse_front = (norm_weight is not None and not reference and not return_intermediates and
+                  block_backend.lower() != "reference" and K_pages.dtype == x2d.dtype and
+                  K_pages.dtype in (torch.float16, torch.bfloat16))
+    if fuse_front:
+        # norm + qkv + RoPE + cache write in one launch, then the attention
+        q, pos = rmsnorm_qkv_rope_paged_update(
+            x2d, norm_weight, qkv_w, qkv_scales, qkv_zeros, K_pages, V_pages, block_table, cos, sin, position,
+            num_attention_heads=H, num_key_value_heads=kv_heads, head_dim=D, bits=bits, group_size=group_size,
+            eps=eps)
+        sc = 1.0 / math.sqrt(D) if scale is None else scale
+        attn_out = _hip_paged_attention(q[:, 0], K_pages, V_pages, _i32(block_table, q.device),
+                                        pos + 1 if lengths is None else lengths, sc).unsqueeze(1)
+    elif norm_weight is not None and not reference:
         qkv = q_rmsnorm_matvec(x2d, norm_weight, qkv_w, qkv_scales, qkv_zeros, bits=bits, group_size=group_size,
                                eps=eps).reshape(x2d.shape[0], 1, -1)
     else:
@@ -198,7 +269,9 @@ def paged_quantized_decode_block(x, qkv_w, qkv_scales, out_w, out_scales, K_page
         qkv = quantized_qkv_projection(x2d, qkv_w, qkv_scales, qkv_zeros, bits=bits, group_size=group_size,
                                        backend=matvec_backend)
     block_fn = reference_paged_gqa_decode_block_from_qkv if block_backend.lower() == "reference" else None
-    if block_fn is not None:
+    if fuse_front:
+        pass
+    elif block_fn is not None:
         attn_out, K_pages, V_pages = block_fn(qkv, K_pages, V_pages, block_table, cos, sin, position,
                                               num_attention_heads=H, num_key_value_heads=kv_heads, head_dim=D,
                                               scale=scale)

@@ -171,3 +171,49 @@ def test_decode_stack_greedy_tokens_vs_oracle(dev):
         cur = got
     # the caches hold every written token, and the positions advanced by one per step
     assert np.array_equal(graph.positions.cpu().numpy(), pos + len(hip_steps))
+
+
+@pytest.mark.parametrize("bits,B", [(4, 1), (4, 3), (8, 1)])
+def test_fused_norm_qkv_rope_paged_matches_two_step(dev, bits, B):
+    """RMSNorm + qkv projection + split + RoPE + paged write in one launch
+    (q4, one row) or the projection-then-update pair otherwise, against the
+    two separate ops on the same inputs: q and every cache byte equal.
+    Rows 1 and 2 of the B = 3 case target one slot (the later row wins)."""
+    from mk import gqa_ops
+    from mk import quantized_decode_block_ops as qd
+    from mk.quant_ops import q_rmsnorm_matvec
+
+    rng = np.random.default_rng(90 + bits + B)
+    cfg, g, P, mb = _cfg(1), 32, 16, 4
+    lw = _np_layer(rng, cfg, bits, g)
+    w = _t_layer(lw, dev, bits, g)
+    Hq, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    K0, V0, bt = _caches(rng, B, mb, P, Hkv, D, 1.0)
+    pos = np.array([5, 37, 37][:B], np.int32)
+    if B == 3:
+        bt[2] = bt[1]  # rows 1 and 2 share the page holding position 37
+    x = torch.from_numpy(rng.standard_normal((B, cfg.hidden_size)).astype(np.float16)).to(dev)
+    cos, sin = op.rope_tables(cfg.max_position_embeddings, D, cfg.rope_theta)
+    tc, ts = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+    btt, post = torch.from_numpy(bt).to(dev), torch.from_numpy(pos).to(dev)
+    Kf, Vf = torch.from_numpy(K0.copy()).to(dev), torch.from_numpy(V0.copy()).to(dev)
+    q, _ = qd.rmsnorm_qkv_rope_paged_update(x, w.input_layernorm_weight, w.qkv_w, w.qkv_scales, w.qkv_zeros, Kf, Vf,
+                                            btt, tc, ts, post, num_attention_heads=Hq, num_key_value_heads=Hkv,
+                                            head_dim=D, bits=bits, group_size=g)
+    Kr, Vr = torch.from_numpy(K0.copy()).to(dev), torch.from_numpy(V0.copy()).to(dev)
+    qkv = q_rmsnorm_matvec(x, w.input_layernorm_weight, w.qkv_w, w.qkv_scales, w.qkv_zeros, bits=bits,
+                           group_size=g)
+    x_, c_, s_, p_, q_ref, _ = gqa_ops._qkv_rope_update_prep(qkv[:, None], btt, tc, ts, post, Hq, Hkv, D, P,
+                                                             torch.float16, dev)
+    from mk import _lib
+    _lib.launch("mk_qkv_rope_paged_update", dev, _lib.ptr(x_), _lib.ptr(c_), _lib.ptr(s_), _lib.ptr(p_),
+                _lib.ptr(btt), _lib.ptr(Kr), _lib.ptr(Vr), _lib.ptr(q_ref), B, Hq, Hkv, D, P, mb, Kr.shape[0],
+                c_.shape[0], _lib.DT_F16)
+    assert torch.equal(q, q_ref), "q"
+    assert torch.equal(Kf, Kr) and torch.equal(Vf, Vr), "caches"
+    # and the cache rows that changed are exactly the written slots
+    changed = (Kf.cpu().numpy() != K0).any(axis=(2, 3))
+    page, off = op.block_table_lookup(bt, pos, P)
+    expect = np.zeros_like(changed)
+    expect[page, off] = True
+    assert np.array_equal(changed, expect)
