@@ -211,8 +211,9 @@ int norm_entry(const void* x, const void* r, const void* w, void* z, void* y, in
 
 // Greedy sampling, models/sampling.py:120-124: per row the index of the
 // largest value, the first one on ties, a NaN counting as the largest (the
-// rule np.argmax follows).  One workgroup per row; threads scan 16-byte
-// chunks, then the (value, index) pairs reduce across lanes and waves.
+// rule np.argmax follows).  One 1024-thread workgroup per row; threads scan
+// 16-byte chunks eight loads at a time, then the (value, index) pairs reduce
+// across lanes and waves.
 __device__ __forceinline__ bool argmax_better(float v, int64_t i, float bv, int64_t bi) {
   if (bv != bv) return v != v && i < bi;
   if (v != v) return true;
@@ -220,27 +221,40 @@ __device__ __forceinline__ bool argmax_better(float v, int64_t i, float bv, int6
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void argmax_rows_kernel(const T* __restrict__ x, int64_t* __restrict__ out,
-                                                          int64_t n, bool vec) {
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const T* __restrict__ x, int64_t* __restrict__ out,
+                                                           int64_t n, bool vec) {
   const T* r = x + (size_t)blockIdx.x * n;
   float bv = -INFINITY;
   int64_t bi = n;  // no candidate yet: any real index is better on ties
+  const int nt = blockDim.x;
   if (vec) {
+    // eight independent 16-byte loads in flight per thread before any compare
     constexpr int EPC = 16 / sizeof(T);  // elements per 16-byte load
+    constexpr int UNR = 8;
     const int64_t nc = n / EPC;
-    for (int64_t c = threadIdx.x; c < nc; c += blockDim.x) {
-      const u32x4 w = ldg128(r + EPC * c);
-      T e[EPC];
-      __builtin_memcpy(e, &w, 16);
+    for (int64_t c0 = 0; c0 < nc; c0 += (int64_t)nt * UNR) {
+      u32x4 w[UNR];
 #pragma unroll
-      for (int k = 0; k < EPC; ++k) {
-        const float v = to_f32(e[k]);
-        const int64_t i = EPC * c + k;
-        if (argmax_better(v, i, bv, bi)) { bv = v; bi = i; }
+      for (int j = 0; j < UNR; ++j) {
+        const int64_t c = c0 + (int64_t)j * nt + threadIdx.x;
+        w[j] = ldg128(r + EPC * (c < nc ? c : nc - 1));
+      }
+#pragma unroll
+      for (int j = 0; j < UNR; ++j) {
+        const int64_t c = c0 + (int64_t)j * nt + threadIdx.x;
+        if (c >= nc) continue;
+        T e[EPC];
+        __builtin_memcpy(e, &w[j], 16);
+#pragma unroll
+        for (int k = 0; k < EPC; ++k) {
+          const float v = to_f32(e[k]);
+          const int64_t i = EPC * c + k;
+          if (argmax_better(v, i, bv, bi)) { bv = v; bi = i; }
+        }
       }
     }
   } else {
-    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+    for (int64_t i = threadIdx.x; i < n; i += nt) {
       const float v = to_f32(r[i]);
       if (argmax_better(v, i, bv, bi)) { bv = v; bi = i; }
     }
@@ -250,13 +264,13 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const T* __restrict__ 
     const int64_t oi = __shfl_xor(bi, d, 64);
     if (argmax_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
   }
-  __shared__ float sv[4];
-  __shared__ int64_t si[4];
+  __shared__ float sv[16];
+  __shared__ int64_t si[16];
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) { sv[wave] = bv; si[wave] = bi; }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+    for (int w = 1; w < (nt >> 6); ++w)
       if (argmax_better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
     out[blockIdx.x] = bi < n ? bi : 0;
   }
@@ -275,11 +289,11 @@ int mk_argmax_rows(const void* x, int64_t* out, int64_t rows, int64_t n, int dty
   // every row starts 16-byte aligned and holds whole 16-byte chunks
   const bool vec = mk_aligned(x, 16) && ((size_t)n * es) % 16 == 0;
   if (dtype == MK_DT_F16)
-    argmax_rows_kernel<f16><<<(unsigned)rows, 256, 0, st>>>((const f16*)x, out, n, vec);
+    argmax_rows_kernel<f16><<<(unsigned)rows, 1024, 0, st>>>((const f16*)x, out, n, vec);
   else if (dtype == MK_DT_BF16)
-    argmax_rows_kernel<bf16><<<(unsigned)rows, 256, 0, st>>>((const bf16*)x, out, n, vec);
+    argmax_rows_kernel<bf16><<<(unsigned)rows, 1024, 0, st>>>((const bf16*)x, out, n, vec);
   else
-    argmax_rows_kernel<float><<<(unsigned)rows, 256, 0, st>>>((const float*)x, out, n, vec);
+    argmax_rows_kernel<float><<<(unsigned)rows, 1024, 0, st>>>((const float*)x, out, n, vec);
   MK_CHECK_LAUNCH();
   return MK_OK;
 }

@@ -94,19 +94,47 @@ __global__ __launch_bounds__(256) void qkv_rope_update_kernel(
 // and store), the q, k and v tasks of a sequence spread over
 // ceil(tasks / 128) workgroups so a small batch still fills several CUs.
 // Same arithmetic and the same skip rules as the scalar kernel.
+constexpr int kRopeSlotMax = 1024;  // batch rows whose slots a workgroup stages in LDS
+
 template <typename T>
 __global__ __launch_bounds__(128) void qkv_rope_update_vec_kernel(
     const T* __restrict__ qkv, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
     const int32_t* __restrict__ pos, const int32_t* __restrict__ bt, T* __restrict__ Kp,
     T* __restrict__ Vp, T* __restrict__ q_out, int B, int Hq, int Hkv, int D, int P,
-    int max_blocks, int num_pages, int cos_rows) {
+    int max_blocks, int num_pages, int cos_rows, bool stage_slots) {
   const int b = blockIdx.x;
   const int cpr = D / 8;  // 8-element chunks per head row
   const int nq = Hq * cpr, nk = Hkv * cpr;
   const int t = (int)blockIdx.y * 128 + (int)threadIdx.x;
+  // every row's cache slot (page * P + offset, -1 when skipped), looked up once
+  // per workgroup with independent loads: the collision rule then reads LDS
+  // instead of walking the later rows' block-table entries one by one
+  __shared__ int slot_lds[kRopeSlotMax];
+  if (stage_slots) {  // workgroup-uniform
+    for (int r = threadIdx.x; r < B; r += blockDim.x) {
+      int o;
+      const int pg = slot_page(bt, pos, r, max_blocks, P, num_pages, &o);
+      slot_lds[r] = pg < 0 ? -1 : pg * P + o;
+    }
+    __syncthreads();
+  }
   if (t >= nq + 2 * nk) return;
   const int p = pos[b];
   if (p < 0 || p >= cos_rows) return;
+  // this row's slot unless out of range or taken by a later row
+  auto my_slot = [&](int* page, int* off) {
+    if (stage_slots) {
+      const int sl = slot_lds[b];
+      if (sl < 0) return false;
+      for (int b2 = b + 1; b2 < B; ++b2)
+        if (slot_lds[b2] == sl) return false;
+      *page = sl / P;
+      *off = sl - *page * P;
+      return true;
+    }
+    *page = slot_page(bt, pos, b, max_blocks, P, num_pages, off);
+    return *page >= 0 && !superseded(bt, pos, b, B, max_blocks, P, num_pages, *page, *off);
+  };
   const T* row = qkv + (size_t)b * (Hq + 2 * Hkv) * D;
   if (t < nq + nk) {
     const bool isq = t < nq;
@@ -133,16 +161,14 @@ __global__ __launch_bounds__(128) void qkv_rope_update_vec_kernel(
       *reinterpret_cast<u32x4*>(q_out + ((size_t)b * Hq + h) * D + 8 * c) = yv;
       return;
     }
-    int off;
-    const int page = slot_page(bt, pos, b, max_blocks, P, num_pages, &off);
-    if (page < 0 || superseded(bt, pos, b, B, max_blocks, P, num_pages, page, off)) return;
+    int page, off;
+    if (!my_slot(&page, &off)) return;
     *reinterpret_cast<u32x4*>(Kp + ((size_t)page * P + off) * Hkv * D + (size_t)h * D + 8 * c) = yv;
     return;
   }
   const int tt = t - nq - nk;  // v chunk
-  int off;
-  const int page = slot_page(bt, pos, b, max_blocks, P, num_pages, &off);
-  if (page < 0 || superseded(bt, pos, b, B, max_blocks, P, num_pages, page, off)) return;
+  int page, off;
+  if (!my_slot(&page, &off)) return;
   *reinterpret_cast<u32x4*>(Vp + ((size_t)page * P + off) * Hkv * D + 8 * (size_t)tt) =
       ldg128(row + (size_t)(Hq + Hkv) * D + 8 * (size_t)tt);
 }
@@ -358,11 +384,12 @@ int mk_qkv_rope_paged_update(const void* qkv, const float* cos_t, const float* s
       mk_aligned(K_pages, 16) && mk_aligned(V_pages, 16) && mk_aligned(cos_t, 16) &&
       mk_aligned(sin_t, 16)) {
     const dim3 grid((unsigned)B, (unsigned)((tasks + 127) / 128));
+    const bool stage = B > 1 && B <= kRopeSlotMax && num_pages * page_size < (1LL << 31);
 #define MK_QRV(T)                                                                                 \
   qkv_rope_update_vec_kernel<T><<<grid, 128, 0, st>>>(                                            \
       (const T*)qkv, cos_t, sin_t, positions, block_table, (T*)K_pages, (T*)V_pages, (T*)q_out, \
       (int)B, (int)Hq, (int)Hkv, (int)D, (int)page_size, (int)max_blocks, (int)num_pages,        \
-      (int)cos_rows)
+      (int)cos_rows, stage)
     if (dtype == MK_DT_F16) MK_QRV(f16);
     else MK_QRV(bf16);
 #undef MK_QRV

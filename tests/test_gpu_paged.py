@@ -254,6 +254,35 @@ def test_qkv_rope_update_bit_exact(dev, dtype, B, Hq, Hkv, D, P, mb):
                  atol=1e-3 if dtype == torch.float16 else 4e-3, what="block attention")
 
 
+@pytest.mark.parametrize("D", [128, 64])
+def test_qkv_rope_update_collisions_and_skips(dev, D):
+    """Batch rows that target one cache slot (the later row's K/V must land)
+    -- the vectorised kernel's staged slot table against the oracle's loop
+    over b."""
+    rng = np.random.default_rng(77 + D)
+    B, Hq, Hkv, P, mb = 7, 8, 2, 16, 4
+    NP = B * mb
+    Kp = _t(rng.standard_normal((NP, P, Hkv, D)), dev, torch.float16)
+    Vp = _t(rng.standard_normal((NP, P, Hkv, D)), dev, torch.float16)
+    bt = rng.permutation(NP).astype(np.int32).reshape(B, mb)
+    pos = rng.integers(0, mb * P, size=B)
+    bt[3] = bt[1]
+    pos[3] = pos[1]          # rows 1 and 3 collide: row 3 wins
+    bt[5] = bt[2]
+    pos[5] = pos[2]
+    bt[6] = bt[2]
+    pos[6] = pos[2]          # rows 2, 5, 6 collide: row 6 wins
+    qkv = _t(rng.standard_normal((B, 1, (Hq + 2 * Hkv) * D)), dev, torch.float16)
+    cos, sin = op.rope_tables(mb * P, D, 500000.0)
+    K0, V0 = Kp.float().cpu().numpy().astype(np.float16), Vp.float().cpu().numpy().astype(np.float16)
+    _, K1, V1 = gqa.paged_gqa_decode_block_from_qkv(
+        qkv, Kp, Vp, to_dev(bt, dev), torch.from_numpy(cos), torch.from_numpy(sin), to_dev(pos, dev),
+        num_attention_heads=Hq, num_key_value_heads=Hkv, head_dim=D)
+    x = qkv[:, 0].cpu().numpy()
+    _, rK, rV = op.qkv_rope_paged_update(x, cos, sin, pos, bt, K0, V0, Hq, Hkv, D)
+    assert np.array_equal(K1.cpu().numpy(), rK) and np.array_equal(V1.cpu().numpy(), rV)
+
+
 def _rope_q(x, cos, sin, pos, Hq, D, dtype):
     q = x[:, :Hq * D].reshape(x.shape[0], Hq, D).astype(np.float32)
     c, s = cos[pos][:, None, :], sin[pos][:, None, :]
