@@ -153,10 +153,12 @@ int mk_q8_rmsnorm_matvec(const void* x, const void* norm_w, float eps, const uin
  * rounding of every stage is that of mk_q*_rmsnorm_matvec followed by
  * mk_qkv_rope_paged_update, so q_out and the caches match that pair exactly.
  * One launch for q4 fp16 (activations, scales, norm weight, pages) with
- * M == 1 and K <= 8192, where qkv_scratch is not written and normed_out may
- * be NULL; otherwise the pair runs, projecting through qkv_scratch [M, (Hq +
- * 2 Hkv) D] and normed_out [M, K] (then required).  K/V pages carry the
- * activation dtype. */
+ * M == 1 and K <= 8192; for other fp16 batches the norm kernel writes
+ * normed_out [M, K] and the projection's epilogue rotates and writes (two
+ * launches); otherwise the projection goes through qkv_scratch [M, (Hq +
+ * 2 Hkv) D] and then mk_qkv_rope_paged_update.  qkv_scratch must be given
+ * (written only on that last path); normed_out is required unless the
+ * one-launch path applies.  K/V pages carry the activation dtype. */
 int mk_q4_rmsnorm_qkv_rope_paged(const void* x, const void* norm_w, float eps, const uint8_t* w, const void* scales,
                                  const void* zeros, void* qkv_scratch, void* normed_out, const float* cos_t,
                                  const float* sin_t, const int32_t* positions, const int32_t* block_table,

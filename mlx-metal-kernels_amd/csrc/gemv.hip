@@ -265,13 +265,35 @@ __device__ __forceinline__ void store_out(const GemvArgs& args, size_t o, float 
   }
 }
 
+// EPI_ROPE_KV: the launch's rows' cache slots (page * P + offset, -1 when
+// skipped), looked up once per workgroup before its reduction barrier, so the
+// later-row-wins rule reads LDS in the epilogue (rows <= 32 per launch).
+constexpr int kRopeRows = 32;
+__device__ __forceinline__ void rope_fill_slots(const GemvArgs& a, int* slots) {
+  const int t = threadIdx.x;
+  if (t < a.M && t < kRopeRows) {
+    const RopeKV& r = a.rk;
+    int off;
+    const int pg = slot_page(r.bt, r.pos, t, r.max_blocks, r.P, r.num_pages, &off);
+    slots[t] = pg < 0 ? -1 : pg * r.P + off;
+  }
+}
+// this row's slot, or -1 when skipped or taken by a later row of the launch
+__device__ __forceinline__ int rope_slot(const GemvArgs& a, const int* slots, int m) {
+  const int sl = slots[m];
+  if (sl < 0) return -1;
+  for (int b2 = m + 1; b2 < a.M; ++b2)
+    if (slots[b2] == sl) return -1;
+  return sl;
+}
+
 // EPI_ROPE_KV: qkv output n of row m, rounded as the projection stores it,
 // then the arithmetic of qkv_rope_update_kernel -- q and k pairs (n, n ^ 1)
 // rotated in fp32 and rounded, v copied; q to q_out, k and v to the token's
 // cache slot unless its position is out of range or a later row takes the
 // slot.  Called by every lane of the pair (the partner value comes by
 // shuffle), whether or not (m, n) is in range.
-__device__ __forceinline__ void rope_kv_store(const GemvArgs& a, int m, int n, float v) {
+__device__ __forceinline__ void rope_kv_store(const GemvArgs& a, const int* slots, int m, int n, float v) {
   const f16 hv = saturate_cast<f16>(v);
   const float xv = to_f32(hv);
   const float xo = __shfl_xor(xv, 1, 64);
@@ -299,10 +321,47 @@ __device__ __forceinline__ void rope_kv_store(const GemvArgs& a, int m, int n, f
   } else {
     h = (n - QD - KD) / D;
   }
-  int off;
-  const int page = slot_page(r.bt, r.pos, m, r.max_blocks, r.P, r.num_pages, &off);
-  if (page < 0 || superseded(r.bt, r.pos, m, a.M, r.max_blocks, r.P, r.num_pages, page, off)) return;
-  dst[((size_t)page * r.P + off) * KD + (size_t)h * D + d] = out;
+  const int sl = rope_slot(a, slots, m);
+  if (sl < 0) return;
+  dst[(size_t)sl * KD + (size_t)h * D + d] = out;
+}
+
+// EPI_ROPE_KV with both values of an (even n, n + 1) pair in one lane (the
+// MFMA kernels' output layout): the same arithmetic as rope_kv_store.
+__device__ __forceinline__ void rope_kv_pair(const GemvArgs& a, const int* slots, int m, int n, float v0,
+                                             float v1) {
+  if (n >= a.N || m >= a.M) return;
+  const RopeKV& r = a.rk;
+  const int p = r.pos[m];
+  if (p < 0 || p >= r.cos_rows) return;
+  const int D = r.D, QD = r.Hq * D, KD = r.Hkv * D;
+  const int d = n % D;
+  const f16 h0 = saturate_cast<f16>(v0), h1 = saturate_cast<f16>(v1);
+  f16 o0 = h0, o1 = h1;
+  f16* dst = reinterpret_cast<f16*>(r.vp);
+  int h;
+  if (n < QD + KD) {
+    const size_t ci = (size_t)p * (D / 2) + (d >> 1);
+    float ye, yo;
+    rope_pair(to_f32(h0), to_f32(h1), r.cos_t[ci], r.sin_t[ci], &ye, &yo);
+    o0 = from_f32<f16>(ye);
+    o1 = from_f32<f16>(yo);
+    if (n < QD) {
+      f16* q = reinterpret_cast<f16*>(r.q_out) + (size_t)m * QD + n;
+      q[0] = o0;
+      q[1] = o1;
+      return;
+    }
+    dst = reinterpret_cast<f16*>(r.kp);
+    h = (n - QD) / D;
+  } else {
+    h = (n - QD - KD) / D;
+  }
+  const int sl = rope_slot(a, slots, m);
+  if (sl < 0) return;
+  f16* o = dst + (size_t)sl * KD + (size_t)h * D + d;
+  o[0] = o0;
+  o[1] = o1;
 }
 
 // --------------------------------------------------------------------------
@@ -431,6 +490,8 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(const GemvArgs args) {
 
   // ---- cross-wave reduction through LDS
   __shared__ f32x4 red[NMAT][8][64];
+  __shared__ int rk_slots[EPI == EPI_ROPE_KV ? kRopeRows : 1];
+  if constexpr (EPI == EPI_ROPE_KV) rope_fill_slots(args, rk_slots);
 #pragma unroll
   for (int t = 0; t < NMAT; ++t) red[t][wave][lane] = acc[t];
   __syncthreads();
@@ -445,6 +506,11 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(const GemvArgs args) {
   // ---- epilogue: lane holds D[n = nb + i][m], i = 0..3
   if (!x_active) return;
   const int nb = n0 + 4 * kb;
+  if constexpr (EPI == EPI_ROPE_KV) {  // fp16 rows; nb is even, the pairs are (nb, nb+1), (nb+2, nb+3)
+    rope_kv_pair(args, rk_slots, m, nb, acc[0][0], acc[0][1]);
+    rope_kv_pair(args, rk_slots, m, nb + 2, acc[0][2], acc[0][3]);
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int nn = nb + i;
@@ -596,6 +662,8 @@ __global__ __launch_bounds__(NMAT == 1 && BITS == 4 ? 1024 : 512) void gemv_tile
   // ---- cross-wave reduction through LDS: [kw][NMAT * MT][64] partial tiles
   extern __shared__ __align__(16) uint8_t tile_red_raw[];
   f32x4* red = reinterpret_cast<f32x4*>(tile_red_raw);
+  __shared__ int rk_slots[EPI == EPI_ROPE_KV ? kRopeRows : 1];
+  if constexpr (EPI == EPI_ROPE_KV) rope_fill_slots(args, rk_slots);
 #pragma unroll
   for (int t = 0; t < NMAT; ++t)
 #pragma unroll
@@ -613,6 +681,11 @@ __global__ __launch_bounds__(NMAT == 1 && BITS == 4 ? 1024 : 512) void gemv_tile
   }
   if (m >= M) return;
   const int nb = n0 + 4 * kb;
+  if constexpr (EPI == EPI_ROPE_KV) {
+    rope_kv_pair(args, rk_slots, m, nb, v[0][0], v[0][1]);
+    rope_kv_pair(args, rk_slots, m, nb + 2, v[0][2], v[0][3]);
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int nn = nb + i;
@@ -1025,6 +1098,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
   for (int d = 32, h = VT / 2; h >= 1; d >>= 1, h >>= 1)
     if (lane & d) idx += h;
   __shared__ float red[8][VT];
+  __shared__ int rk_slots[EPI == EPI_ROPE_KV ? kRopeRows : 1];
+  if constexpr (EPI == EPI_ROPE_KV) rope_fill_slots(args, rk_slots);
   constexpr int QUAD = 64 / VT;  // lanes holding the same index
   if ((lane & (QUAD - 1)) == 0) red[wave][idx] = tot;
   __syncthreads();
@@ -1037,7 +1112,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
   }
   const int nn = n0 + rr;
   if constexpr (EPI == EPI_ROPE_KV) {
-    rope_kv_store(args, m, nn, v0);  // lane pairs (rr even, rr + 1) never straddle a head: R and D even
+    rope_kv_store(args, rk_slots, m, nn, v0);  // lane pairs (rr even, rr + 1) never straddle a head: R and D even
     return;
   }
   if (nn < N && m < args.M) store_out<f16, EPI>(args, (size_t)m * N + nn, v0, v1);
@@ -1275,6 +1350,25 @@ int gemv_dispatch(GemvArgs a, int64_t M, int64_t N, int64_t K, int64_t gs, int a
 
   const size_t xe = 2;  // activation element size
   int rc = MK_OK;
+  // rows m0.. of every row-indexed operand
+  auto rows_from = [&](GemvArgs& b, int64_t m0) {
+    b.x = (const char*)a.x + (size_t)m0 * K * xe;
+    if (a.residual) b.residual = (const char*)a.residual + (size_t)m0 * N * xe;
+    if (a.y0) b.y0 = (char*)a.y0 + (size_t)m0 * N * xe;
+    if (a.y1) b.y1 = (char*)a.y1 + (size_t)m0 * N * xe;
+    if (a.y2) b.y2 = (char*)a.y2 + (size_t)m0 * N * xe;
+    if constexpr (EPI == EPI_ROPE_KV) {
+      // rows of a later pass write after this one: the later row of a
+      // colliding pair still wins
+      b.rk.pos = a.rk.pos + m0;
+      b.rk.bt = a.rk.bt + (size_t)m0 * a.rk.max_blocks;
+      b.rk.q_out = (char*)a.rk.q_out + (size_t)m0 * a.rk.Hq * a.rk.D * xe;
+    }
+  };
+  if constexpr (EPI == EPI_ROPE_KV) {
+    // fp16 projections on the fast layouts only (the caller falls back)
+    if (act_dt != MK_DT_F16 || sc_dt != MK_DT_F16 || !fast) return MK_ERR_UNSUPPORTED;
+  }
   // 17-32 rows at a time through the two-column-tile kernel, the rest below
   int64_t m_done = 0;
   if (tile_eligible<NMAT>(a, act_dt, sc_dt)) {
@@ -1282,11 +1376,7 @@ int gemv_dispatch(GemvArgs a, int64_t M, int64_t N, int64_t K, int64_t gs, int a
       GemvArgs b = a;
       const int64_t mrows = (M - m_done) < 32 ? (M - m_done) : 32;
       b.M = (int)mrows;
-      b.x = (const char*)a.x + (size_t)m_done * K * xe;
-      if (a.residual) b.residual = (const char*)a.residual + (size_t)m_done * N * xe;
-      if (a.y0) b.y0 = (char*)a.y0 + (size_t)m_done * N * xe;
-      if (a.y1) b.y1 = (char*)a.y1 + (size_t)m_done * N * xe;
-      if (a.y2) b.y2 = (char*)a.y2 + (size_t)m_done * N * xe;
+      rows_from(b, m_done);
       rc = launch_tile<BITS, NMAT, 2, EPI>(b, st);
       m_done += mrows;
     }
@@ -1297,14 +1387,13 @@ int gemv_dispatch(GemvArgs a, int64_t M, int64_t N, int64_t K, int64_t gs, int a
     const int64_t m0 = m_done + mb * 16;
     const int64_t mrows = (M - m0) < 16 ? (M - m0) : 16;
     b.M = (int)mrows;
-    b.x = (const char*)a.x + (size_t)m0 * K * xe;
-    if (a.residual) b.residual = (const char*)a.residual + (size_t)m0 * N * xe;
-    if (a.y0) b.y0 = (char*)a.y0 + (size_t)m0 * N * xe;
-    if (a.y1) b.y1 = (char*)a.y1 + (size_t)m0 * N * xe;
-    if (a.y2) b.y2 = (char*)a.y2 + (size_t)m0 * N * xe;
+    rows_from(b, m0);
     if (dot_eligible<BITS, NMAT>(b, fast && mk_aligned(b.x, 16), mrows, act_dt, sc_dt)) {
       b.kw = dot_waves(K);
       rc = launch_dot<BITS, NMAT, EPI>(b, st);
+    } else if constexpr (EPI == EPI_ROPE_KV) {
+      b.kw = choose_kw(N, K, F::KC);
+      rc = launch_fast<BITS, f16, f16, true, NMAT, EPI>(b, gpc, st);
     } else if (fast) {
       b.kw = choose_kw(N, K, F::KC);
       if (act_dt == MK_DT_F16 && sc_dt == MK_DT_F16)
@@ -1488,7 +1577,7 @@ int norm_qkv_rope_entry(const void* x, const void* norm_w, float eps, const uint
              V_pages && q_out);
   MK_REQUIRE(M >= 0 && M < 65536 && Hq > 0 && Hkv > 0 && D > 0 && (D % 2) == 0 && P > 0 && max_blocks > 0 &&
              num_pages > 0 && cos_rows > 0 && K > 0 && gs > 0);
-  MK_REQUIRE((Hq + 2 * Hkv) * D < (1LL << 31) && num_pages < (1LL << 31) && max_blocks * P < (1LL << 31));
+  MK_REQUIRE((Hq + 2 * Hkv) * D < (1LL << 31) && num_pages * P < (1LL << 31) && max_blocks * P < (1LL << 31));
   MK_REQUIRE(act_dt == MK_DT_F16 || act_dt == MK_DT_BF16);
   if (M == 0) return MK_OK;
   const int64_t N = (Hq + 2 * Hkv) * D;
@@ -1513,6 +1602,25 @@ int norm_qkv_rope_entry(const void* x, const void* norm_w, float eps, const uint
       a.rk = RopeKV{cos_t, sin_t, positions, block_table, K_pages, V_pages, q_out, (int)Hq, (int)Hkv, (int)D,
                     (int)P, (int)max_blocks, (int)num_pages, (int)cos_rows};
       return launch_dot<BITS, 1, EPI_ROPE_KV, true>(a, reinterpret_cast<hipStream_t>(stream));
+    }
+  }
+  MK_REQUIRE(normed_out);  // the multi-launch paths pass the normalised rows through it
+  if (act_dt == MK_DT_F16 && sc_dt == MK_DT_F16 && max_blocks * P < (1LL << 31)) {
+    // the norm kernel, then the projection whose epilogue rotates and writes
+    GemvArgs a = {};
+    a.x = normed_out;
+    a.w[0] = a.w[1] = w;
+    a.s[0] = a.s[1] = s;
+    a.z[0] = a.z[1] = z;
+    a.rk = RopeKV{cos_t, sin_t, positions, block_table, K_pages, V_pages, q_out, (int)Hq, (int)Hkv, (int)D,
+                  (int)P, (int)max_blocks, (int)num_pages, (int)cos_rows};
+    GemvArgs probe = a;
+    bool fast;
+    gemv_prepare<BITS, 1>(probe, N, K, gs, &fast);
+    if (fast) {
+      int rc = mk_rms_norm(x, norm_w, normed_out, M, K, eps, act_dt, nw_dt, stream);
+      if (rc != MK_OK) return rc;
+      return gemv_dispatch<BITS, 1, EPI_ROPE_KV>(a, M, N, K, gs, act_dt, sc_dt, reinterpret_cast<hipStream_t>(stream));
     }
   }
   const int rc = norm_matvec_entry<BITS>(x, norm_w, eps, w, s, z, normed_out, qkv_scratch, M, N, K, gs, act_dt,

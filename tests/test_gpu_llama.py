@@ -173,12 +173,14 @@ def test_decode_stack_greedy_tokens_vs_oracle(dev):
     assert np.array_equal(graph.positions.cpu().numpy(), pos + len(hip_steps))
 
 
-@pytest.mark.parametrize("bits,B", [(4, 1), (4, 3), (8, 1)])
+@pytest.mark.parametrize("bits,B", [(4, 1), (4, 2), (4, 3), (4, 8), (4, 20), (4, 33), (8, 1), (8, 4), (8, 20)])
 def test_fused_norm_qkv_rope_paged_matches_two_step(dev, bits, B):
-    """RMSNorm + qkv projection + split + RoPE + paged write in one launch
-    (q4, one row) or the projection-then-update pair otherwise, against the
-    two separate ops on the same inputs: q and every cache byte equal.
-    Rows 1 and 2 of the B = 3 case target one slot (the later row wins)."""
+    """RMSNorm + qkv projection + split + RoPE + paged write -- one launch for
+    one q4 row, else the norm kernel then a projection (v_dot2 rows, MFMA,
+    two-column tiles, in passes past 32 rows) whose epilogue rotates and
+    writes -- against the separate norm + projection + update ops on the same
+    inputs: q and every cache byte equal.  From B = 3 on, rows 1 and 2 target
+    one slot (the later row wins)."""
     from mk import gqa_ops
     from mk import quantized_decode_block_ops as qd
     from mk.quant_ops import q_rmsnorm_matvec
@@ -189,9 +191,10 @@ def test_fused_norm_qkv_rope_paged_matches_two_step(dev, bits, B):
     w = _t_layer(lw, dev, bits, g)
     Hq, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
     K0, V0, bt = _caches(rng, B, mb, P, Hkv, D, 1.0)
-    pos = np.array([5, 37, 37][:B], np.int32)
-    if B == 3:
-        bt[2] = bt[1]  # rows 1 and 2 share the page holding position 37
+    pos = rng.integers(0, mb * P, size=B).astype(np.int32)
+    if B >= 3:
+        bt[2] = bt[1]  # rows 1 and 2 share the page holding one position
+        pos[2] = pos[1]
     x = torch.from_numpy(rng.standard_normal((B, cfg.hidden_size)).astype(np.float16)).to(dev)
     cos, sin = op.rope_tables(cfg.max_position_embeddings, D, cfg.rope_theta)
     tc, ts = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
