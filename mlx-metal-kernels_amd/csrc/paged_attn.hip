@@ -131,13 +131,21 @@ __device__ __forceinline__ u32x4 deq8x8(uint32_t u0, uint32_t u1, f16x2 s2) {
   r[3] = q8_pair(u1, 8, s2);
   return r;
 }
-// 8 q4 codes (one word) -> 8 fp16, order [0,4,1,5,2,6,3,7]
+// 8 q4 codes (one word) -> 8 fp16, order [0,4,1,5,2,6,3,7].  Odd nibbles
+// stay in place: (1024 + 16 c) - (1024 + 128) = 16 (c - 8) exactly, times
+// s / 16 -- the same product (c - 8) s whenever s / 16 is a normal fp16
+// (s >= 2^-10), one shift per word instead of three.
 __device__ __forceinline__ u32x4 deq4x8(uint32_t u, f16x2 s2) {
+  const f16x2 k_lo = {(f16)1032.0f, (f16)1032.0f};  // 1024 + 8
+  const f16x2 k_hi = {(f16)1152.0f, (f16)1152.0f};  // 1024 + 16 * 8
+  const f16x2 s16 = s2 * (f16x2){(f16)0.0625f, (f16)0.0625f};
+  const uint32_t magic = 0x64006400u;
+  const uint32_t v = u >> 8;
   u32x4 r;
-  r[0] = q4_pair(u, 0, s2);
-  r[1] = q4_pair(u, 4, s2);
-  r[2] = q4_pair(u, 8, s2);
-  r[3] = q4_pair(u, 12, s2);
+  r[0] = bitcast<uint32_t>((bitcast<f16x2>((u & 0x000F000Fu) | magic) - k_lo) * s2);
+  r[1] = bitcast<uint32_t>((bitcast<f16x2>((u & 0x00F000F0u) | magic) - k_hi) * s16);
+  r[2] = bitcast<uint32_t>((bitcast<f16x2>((v & 0x000F000Fu) | magic) - k_lo) * s2);
+  r[3] = bitcast<uint32_t>((bitcast<f16x2>((v & 0x00F000F0u) | magic) - k_hi) * s16);
   return r;
 }
 
