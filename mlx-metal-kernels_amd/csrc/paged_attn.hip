@@ -113,7 +113,9 @@ __device__ __forceinline__ uint32_t pack_act2(float lo, float hi) {
 // fp32 product rounded to fp16.
 __device__ __forceinline__ uint32_t q8_pair(uint32_t u, int shift, f16x2 s2) {
   const f16x2 k = {(f16)1152.0f, (f16)1152.0f};  // 1024 + 128
-  f16x2 v = bitcast<f16x2>(((u >> shift) & 0x00FF00FFu) | 0x64006400u) - k;
+  // bytes (b0|b1, 0x64, b2|b3, 0x64) of {0x64646464, u}: one v_perm_b32
+  const uint32_t t = perm_b32(0x64646464u, u, shift == 0 ? 0x04020400u : 0x04030401u);
+  f16x2 v = bitcast<f16x2>(t) - k;
   return bitcast<uint32_t>(v * s2);
 }
 __device__ __forceinline__ uint32_t q4_pair(uint32_t u, int shift, f16x2 s2) {
