@@ -225,6 +225,46 @@ def attention_config3(dev, steps, warmup):
     }
 
 
+def attention_config4(dev, steps=30, warmup=5):
+    """paged GQA decode over q8 and q4 KV, B=8 at context
+    32768, Hq 32 / Hkv 8, D in (128, 64), P=16, groups of 64 with fp16 scales;
+    random codes and scales (the kernel's work does not depend on the values),
+    a seeded random block table.  Bytes = the codes and scales of every
+    position read."""
+    import torch
+
+    import mk.paged_quantized_kv_ops as pq
+
+    B, Hq, Hkv, P, ctx, g = 8, 32, 8, 16, 32768, 64
+    mb = ctx // P
+    NP = B * mb
+    out = {"workload": "config4_paged_gqa_q8_q4_B8_ctx32768_g64"}
+    for D in (128, 64):
+        for bits in (8, 4):
+            cols = D if bits == 8 else D // 2
+            gen = torch.Generator(device=dev)
+            gen.manual_seed(7)
+            kq = torch.randint(0, 256, (NP, P, Hkv, cols), dtype=torch.uint8, device=dev, generator=gen)
+            vq = torch.randint(0, 256, (NP, P, Hkv, cols), dtype=torch.uint8, device=dev, generator=gen)
+            ks = (torch.rand((NP, P, Hkv, D // g), device=dev, generator=gen) * 0.2 + 0.05).half()
+            vs = (torch.rand((NP, P, Hkv, D // g), device=dev, generator=gen) * 0.2 + 0.05).half()
+            bt = torch.randperm(NP, device=dev, generator=gen).to(torch.int32).reshape(B, mb)
+            ln = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+            cache = pq.PagedQuantizedKVCache(k_pages_q=kq, v_pages_q=vq, k_scales=ks, v_scales=vs, block_table=bt,
+                                             lengths=ln, bits=bits, page_size=P, group_size=g,
+                                             original_page_shape=(NP, P, Hkv, D))
+            q = torch.randn((B, 1, Hq, D), device=dev).half()
+            fns = [lambda: pq.paged_quantized_kv_gqa_decode_attention(q, cache, backend=f"metal_q{bits}")]
+            ms = time_steps(fns, steps, warmup)
+            nbytes = B * ctx * Hkv * 2 * (cols + (D // g) * 2)
+            out[f"D{D}_q{bits}"] = {"us_per_call": ms * 1e3, "tokens_per_s": B / (ms * 1e-3),
+                                   "hbm_gbs": nbytes / (ms * 1e-3) / 1e9,
+                                   "frac_of_peak": nbytes / (ms * 1e-3) / 1e9 / PEAK_GBS, "bytes": nbytes}
+            del cache, kq, vq, ks, vs, fns
+            torch.cuda.empty_cache()
+    return out
+
+
 def decode_stack_config5(dev, batches=(1, 32), steps=128, ctx=2048):
     """Llama-3-8B shape (32 layers, hidden 4096, 32/8
     heads of 128, intermediate 14336), every projection and the head q4 g64
@@ -428,6 +468,7 @@ def main():
             torch.cuda.empty_cache()
         torch.cuda.empty_cache()
         extra["paged_attention"] = attention_config3(dev, max(50, args.steps // 3), 10)
+        extra["quantized_attention"] = attention_config4(dev)
         extra["decode_stack"] = decode_stack_config5(dev)
 
     cpu = None
