@@ -235,8 +235,15 @@ __device__ __forceinline__ u32x2 deq8x4(uint32_t u, f16x2 s2) {
   return (u32x2){q8_pair(u, 0, s2), q8_pair(u, 8, s2)};
 }
 __device__ __forceinline__ u32x2 deq4x4(uint32_t u, f16x2 s2) {
-  const uint32_t t = (u & 0xFFu) | ((u & 0xFF00u) << 8);  // n0 n1 @ bits 0..7, n2 n3 @ 16..23
-  return (u32x2){q4_pair(t, 0, s2), q4_pair(t, 4, s2)};
+  // bytes (b0, 0, b1, 0): n0 n1 @ bits 0..7, n2 n3 @ 16..23, one v_perm_b32;
+  // the odd nibbles stay in place against s / 16 as in deq4x8
+  const uint32_t t = perm_b32(0u, u, 0x04010400u);
+  const f16x2 k_lo = {(f16)1032.0f, (f16)1032.0f};
+  const f16x2 k_hi = {(f16)1152.0f, (f16)1152.0f};
+  const f16x2 s16 = s2 * (f16x2){(f16)0.0625f, (f16)0.0625f};
+  const uint32_t magic = 0x64006400u;
+  return (u32x2){bitcast<uint32_t>((bitcast<f16x2>((t & 0x000F000Fu) | magic) - k_lo) * s2),
+                 bitcast<uint32_t>((bitcast<f16x2>((t & 0x00F000F0u) | magic) - k_hi) * s16)};
 }
 
 __device__ __forceinline__ f16x2 splat_h(uint32_t s) {
