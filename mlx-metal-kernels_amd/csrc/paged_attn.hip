@@ -35,10 +35,10 @@ constexpr int kBlockPos = 32;         // positions per softmax block (two MFMA t
 constexpr int kMaxSplitPages = 512;   // page ids one split may touch (LDS)
 
 // Fewest 32-position blocks per pair: below it a wave's fixed start-up cost
-// outweighs the extra parallelism.
-#ifndef MK_ATTN_MIN_SPLIT_BLOCKS
-#define MK_ATTN_MIN_SPLIT_BLOCKS 4
-#endif
+// outweighs the extra parallelism.  Measured (config 3 fp16 / config 4):
+// 8 for fp16 and q4 pages (config 3 56.7 -> 54.0 us), 4 for q8 (8 cost it 2 %).
+constexpr int kMinSplitBlocks16 = 8;
+constexpr int kMinSplitBlocksQ8 = 4;
 // Segments per pair whose q is staged in LDS at start-up (a pair crossing
 // more sequences loads the rest when it reaches them).
 #ifndef MK_ATTN_QSLOTS
@@ -79,6 +79,7 @@ struct PagedArgs {
   // waves, the most blocks one pair may hold, and the pair count bound the
   // workspace and the grid are sized for
   int T_pairs, cap_blk, max_pairs;
+  int min_split;       // fewest blocks per pair
   int units;           // (kv head, block of 16 query heads) waves per pair
   int wg_units;        // units per workgroup (a divisor of units, <= 8)
   float scale_log2;
@@ -270,7 +271,7 @@ struct KVBlock {
 // lengths; a CU's time is the bytes of the waves it holds, so equal pairs
 // keep every CU busy to the end.  N is one round of resident waves
 // (T_pairs), fewer when the pairs would hold less than
-// MK_ATTN_MIN_SPLIT_BLOCKS blocks, more when they would exceed cap_blk (the
+// min_split blocks (by KV format), more when they would exceed cap_blk (the
 // blocks whose pages one wave can address).  A pair that crosses a sequence
 // boundary works on one segment per sequence it touches.  A segment that
 // covers its whole sequence writes the output; any other writes a partial
@@ -331,7 +332,7 @@ __device__ StreamPlan stream_plan(const PagedArgs& a, int lane) {
   sp.TB = wave_sum_i64(tb);
   sp.start0 = (int)(wave_incl_scan_i64(nb0, lane) - nb0);
   int64_t N = a.T_pairs;
-  const int64_t minb = MK_ATTN_MIN_SPLIT_BLOCKS < a.cap_blk ? MK_ATTN_MIN_SPLIT_BLOCKS : a.cap_blk;
+  const int64_t minb = a.min_split < a.cap_blk ? a.min_split : a.cap_blk;
   if (sp.TB < N * minb) N = (sp.TB + minb - 1) / minb;
   if (N > 0 && (sp.TB + N - 1) / N > a.cap_blk) N = (sp.TB + a.cap_blk - 1) / a.cap_blk;
   if (N > sp.TB) N = sp.TB;
@@ -1240,7 +1241,7 @@ inline bool fast_ok(int64_t D, int kvf, int dtype, int64_t gs, int64_t P, int64_
 // Host half of the stream plan: workgroup shape, pairs per round (one per
 // resident wave slot: two waves per SIMD, four SIMDs per CU), the most
 // blocks one pair may hold, and the pair count bound.
-inline void split_plan(PagedArgs& a) {
+inline void split_plan(PagedArgs& a, int kvf) {
   a.units = a.Hkv * a.HB;
   const int64_t cus = device_cus();
   int64_t T = cus * 8 / a.units;
@@ -1262,7 +1263,8 @@ inline void split_plan(PagedArgs& a) {
   // The units of a pair share a workgroup (up to 8 waves, one CU) when the
   // block table allows enough pairs for a workgroup per CU; with fewer pairs
   // (short total context) one-wave workgroups spread them over all CUs.
-  const int64_t minb = MK_ATTN_MIN_SPLIT_BLOCKS < cap ? MK_ATTN_MIN_SPLIT_BLOCKS : cap;
+  a.min_split = kvf == 8 ? kMinSplitBlocksQ8 : kMinSplitBlocks16;
+  const int64_t minb = a.min_split < cap ? a.min_split : cap;
   int64_t pairs = (a.B * blk_per_seq + minb - 1) / minb;
   if (pairs > T) pairs = T;
   int wg = 1;
@@ -1288,7 +1290,7 @@ int attention_launch(PagedArgs a, int64_t D, int kvf, int dtype, size_t ws_bytes
   if (fast) {
     a.lgP = ilog2(a.P);
     a.lg_gs = kvf ? ilog2(a.gs) : 0;
-    split_plan(a);
+    split_plan(a, kvf);
     const size_t need = workspace_need(a, D);
     if (!a.ws || ws_bytes < need || !mk_aligned(a.ws, 16)) return MK_ERR_INVALID;
     a.ws_ml = a.ws + (size_t)workspace_slots(a) * a.Hq * D;
@@ -1368,7 +1370,7 @@ size_t mk_paged_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, in
   a.HB = (a.G + 15) / 16;
   a.P = (int)page_size;
   a.MB = (int)max_blocks;
-  split_plan(a);
+  split_plan(a, 0);  // the workspace does not depend on the format
   return workspace_need(a, D);
 }
 
