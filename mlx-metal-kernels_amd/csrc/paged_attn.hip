@@ -39,6 +39,12 @@ constexpr int kMaxSplitPages = 512;   // page ids one split may touch (LDS)
 // 8 for fp16 and q4 pages (config 3 56.7 -> 54.0 us), 4 for q8 (8 cost it 2 %).
 constexpr int kMinSplitBlocks16 = 8;
 constexpr int kMinSplitBlocksQ8 = 4;
+// A short total context shortens the pairs, down to kMinSplitFloor blocks, so
+// that kMinPairs of them run at once: a short pair's time is mostly the
+// dependent lengths -> table -> page latency at its start, not its bytes
+// (one 2048-position sequence: 8 pairs 17.3 us, 32 pairs 13.3 us per call).
+constexpr int kMinPairs = 32;
+constexpr int kMinSplitFloor = 2;
 // Segments per pair whose q is staged in LDS at start-up (a pair crossing
 // more sequences loads the rest when it reaches them).
 #ifndef MK_ATTN_QSLOTS
@@ -271,7 +277,9 @@ struct KVBlock {
 // lengths; a CU's time is the bytes of the waves it holds, so equal pairs
 // keep every CU busy to the end.  N is one round of resident waves
 // (T_pairs), fewer when the pairs would hold less than
-// min_split blocks (by KV format), more when they would exceed cap_blk (the
+// min_split blocks (by KV format; less on a short total context, down to
+// kMinSplitFloor, while fewer than kMinPairs pairs would run), more when they
+// would exceed cap_blk (the
 // blocks whose pages one wave can address).  A pair that crosses a sequence
 // boundary works on one segment per sequence it touches.  A segment that
 // covers its whole sequence writes the output; any other writes a partial
@@ -332,7 +340,10 @@ __device__ StreamPlan stream_plan(const PagedArgs& a, int lane) {
   sp.TB = wave_sum_i64(tb);
   sp.start0 = (int)(wave_incl_scan_i64(nb0, lane) - nb0);
   int64_t N = a.T_pairs;
-  const int64_t minb = a.min_split < a.cap_blk ? a.min_split : a.cap_blk;
+  int64_t minb = a.min_split < a.cap_blk ? a.min_split : a.cap_blk;
+  const int64_t want = sp.TB / kMinPairs;  // blocks per pair at kMinPairs pairs
+  if (want < minb) minb = want > kMinSplitFloor ? want : kMinSplitFloor;
+  if (minb > a.cap_blk) minb = a.cap_blk;
   if (sp.TB < N * minb) N = (sp.TB + minb - 1) / minb;
   if (N > 0 && (sp.TB + N - 1) / N > a.cap_blk) N = (sp.TB + a.cap_blk - 1) / a.cap_blk;
   if (N > sp.TB) N = sp.TB;
