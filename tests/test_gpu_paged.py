@@ -144,6 +144,22 @@ def test_paged_attention_pairs_at_block_cap(dev):
     assert_close(got, ref, rtol=1e-2, atol=1e-3, what="long context")
 
 
+@pytest.mark.parametrize("lengths", [[64], [2047], [2048], [2049], [95, 1, 2000], [8191], [8224]])
+def test_paged_attention_short_context_split(dev, lengths):
+    """A short total context shortens the pairs of the stream plan (down to two
+    32-position blocks) so that 32 of them run; the block totals straddle the
+    points where that minimum changes (64 and 256 blocks), and a single pair
+    covering its whole sequence is written without the merge."""
+    B, Hq, Hkv, D, P = len(lengths), 32, 8, 128, 16
+    mb = (max(lengths) + P - 1) // P
+    q, Kp, Vp, bt, lengths = _case(31 + sum(lengths), B, Hq, Hkv, D, P, mb, lengths=lengths)
+    qt, Kt, Vt = (_t(a, dev, torch.float16) for a in (q, Kp, Vp))
+    got = gqa.paged_gqa_decode_attention(qt[:, None], Kt, Vt, to_dev(bt, dev), to_dev(lengths, dev))[:, 0]
+    ref = op.paged_attention(qt.float().cpu().numpy(), Kt.float().cpu().numpy(), Vt.float().cpu().numpy(), bt,
+                             lengths)
+    assert_close(got, ref, rtol=1e-2, atol=1e-3, what=f"short context {lengths.tolist()}")
+
+
 def test_paged_attention_graph_replays(dev):
     """The one-kernel attention captured in a HIP graph: every replay, with
     eager calls and synchronisations between them, equals the eager result."""
