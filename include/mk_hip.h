@@ -115,7 +115,7 @@ int mk_q8_gate_up(const void* x, const uint8_t* w_gate, const uint8_t* w_up,
  * fp16 norm weights and fp16 scales this is one launch (the norm runs inside
  * the gate/up kernel) and normed_out may be NULL; otherwise the norm kernel
  * and the gate/up kernel run in turn through normed_out, which is then
- * required (MK_ERR_ARG when NULL).
+ * required (MK_ERR_INVALID when NULL).
  * norm_w_dtype: MK_DT_F16/BF16/F32. */
 int mk_q4_rmsnorm_gate_up(const void* x, const void* residual, const void* norm_w, float eps,
                           const uint8_t* w_gate, const uint8_t* w_up, const void* s_gate, const void* s_up,

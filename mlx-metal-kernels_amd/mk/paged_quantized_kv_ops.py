@@ -363,9 +363,38 @@ def reference_paged_quantized_kv_gqa_decode_attention(q, paged_qkv: PagedQuantiz
     return _masked_attention(q[:, 0], Kc, Vc, lengths_arr, valid, scale).unsqueeze(1).to(q.dtype)
 
 
+def _check_kernel_layout(paged_qkv: PagedQuantizedKVCache, Hkv: int, D: int) -> int:
+    """The kernels index codes and scales from (num_pages, page_size, Hkv, D,
+    bits, group_size) alone, so the tensors must have exactly that layout:
+    codes [NP, P, Hkv, D] (q8) or [NP, P, Hkv, ceil(D/2)] (q4), scales
+    [NP, P, Hkv, ceil(D/group_size)].  Returns NP, taken from the tensors."""
+    P, g = int(paged_qkv.page_size), int(paged_qkv.group_size)
+    if paged_qkv.bits not in (4, 8):
+        raise ValueError(f"bits must be 4 or 8, got {paged_qkv.bits}")
+    if P <= 0 or g <= 0:
+        raise ValueError(f"page_size and group_size must be positive, got {P}, {g}")
+    if paged_qkv.k_pages_q.ndim != 4:
+        raise ValueError(f"k_pages_q must be 4-D [NUM_PAGES,PAGE_SIZE,Hkv,Dq], got {tuple(paged_qkv.k_pages_q.shape)}")
+    NP = int(paged_qkv.k_pages_q.shape[0])
+    Dq = D if paged_qkv.bits == 8 else (D + 1) // 2
+    want_codes = (NP, P, Hkv, Dq)
+    want_scales = (NP, P, Hkv, (D + g - 1) // g)
+    for name, t, want in (("k_pages_q", paged_qkv.k_pages_q, want_codes), ("v_pages_q", paged_qkv.v_pages_q, want_codes),
+                          ("k_scales", paged_qkv.k_scales, want_scales), ("v_scales", paged_qkv.v_scales, want_scales)):
+        if tuple(t.shape) != want:
+            raise ValueError(f"{name} must have shape {want} for bits={paged_qkv.bits}, page_size={P}, Hkv={Hkv}, "
+                             f"D={D}, group_size={g}; got {tuple(t.shape)}")
+    orig = paged_qkv.original_page_shape
+    if orig is not None and tuple(orig[1:]) != (P, Hkv, D):
+        raise ValueError(f"original_page_shape {tuple(orig)} disagrees with page_size={P}, Hkv={Hkv}, D={D}")
+    return NP
+
+
 def _hip_quantized_attention(q, paged_qkv: PagedQuantizedKVCache, lengths_arr, scale: float):
     B, _, Hq, D = q.shape
-    NUM_PAGES, PAGE_SIZE, Hkv, _ = paged_qkv.original_page_shape
+    _, _, Hkv, _ = paged_qkv.original_page_shape
+    PAGE_SIZE = int(paged_qkv.page_size)
+    NUM_PAGES = _check_kernel_layout(paged_qkv, Hkv, D)
     MAX_BLOCKS = paged_qkv.block_table.shape[1]
     kq = paged_qkv.k_pages_q.contiguous()
     vq = paged_qkv.v_pages_q.contiguous()
@@ -475,9 +504,10 @@ def paged_quantized_kv_update_from_qkv(qkv, paged_qkv: PagedQuantizedKVCache, co
         raise TypeError("quantized pages must be uint8")
     if Hkv * D > 4096:
         raise ValueError(f"fused quantized update supports Hkv*D <= 4096, got {Hkv * D}")
+    NUM_PAGES = _check_kernel_layout(paged_qkv, Hkv, D)
+    P = int(paged_qkv.page_size)
     dtype = qkv.dtype if qkv.dtype in (torch.float16, torch.bfloat16) else torch.float16
     dev = _lib.require_device(qkv, paged_qkv.k_pages_q, paged_qkv.v_pages_q, paged_qkv.k_scales, paged_qkv.v_scales)
-    NUM_PAGES, P = paged_qkv.k_pages_q.shape[0], paged_qkv.page_size
     MAX_BLOCKS = paged_qkv.block_table.shape[1]
     x, c, s, pos, q_out, B = _qkv_rope_update_prep(qkv, paged_qkv.block_table, cos, sin, position, Hq, Hkv, D, P,
                                                    dtype, dev)

@@ -25,11 +25,6 @@ import torch
 from . import _lib
 from ._common import ACT_DTYPES, as_u8, ci_safe_mode_enabled, finfo_max, scales_for_kernel
 
-_THREADS = 256
-_MATVEC_PARALLEL_THREADS = 128
-_MATVEC_TILED_THREADS = 128
-_MATVEC_N_TILE = 4
-
 _MATVEC_BACKENDS_MSG = "backend must be one of 'reference', 'metal', 'metal_parallel', 'metal_tiled', 'auto'"
 
 

@@ -237,6 +237,48 @@ def test_host_quantize_kv_pages_bit_exact(bits):
     assert c.memory_bytes() == expect
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantized_cache_layout_checked_before_launch(bits):
+    # metadata that overstates pages / page size / Hkv, or codes and scales in
+    # another layout, must raise ValueError on the host before any pointer is
+    # handed to a kernel (host tensors: reaching require_device would raise a
+    # different ValueError, about the device).
+    import dataclasses
+
+    NP, P, Hkv, D, g, B, Hq = 4, 4, 2, 64, 32, 2, 4
+    Kp = torch.randn(NP, P, Hkv, D).to(torch.float16)
+    cfg = pq.PagedQuantizedKVConfig(bits=bits, page_size=P, group_size=g)
+    bt = torch.arange(NP, dtype=torch.int32).reshape(B, NP // B)
+    c = pq.quantize_kv_pages(Kp, Kp.clone(), bt, torch.tensor([5, 8], dtype=torch.int32), cfg)
+    q = torch.randn(B, 1, Hq, D).to(torch.float16)
+    backend = f"metal_q{bits}"
+    other = 4 if bits == 8 else 8
+    cases = {
+        "page_size": dataclasses.replace(c, page_size=2 * P, original_page_shape=(NP, 2 * P, Hkv, D)),
+        "Hkv": dataclasses.replace(c, original_page_shape=(NP, P, 2 * Hkv, D)),
+        "group": dataclasses.replace(c, group_size=g // 2),
+        "codes": dataclasses.replace(c, k_pages_q=c.k_pages_q[..., : c.k_pages_q.shape[-1] // 2].contiguous(),
+                                     v_pages_q=c.v_pages_q[..., : c.v_pages_q.shape[-1] // 2].contiguous()),
+        "pages": dataclasses.replace(c, k_scales=c.k_scales[:2].contiguous(), v_scales=c.v_scales[:2].contiguous()),
+    }
+    for what, bad in cases.items():
+        with pytest.raises(ValueError, match="must have shape|disagrees|must be"):
+            pq.paged_quantized_kv_gqa_decode_attention(q, bad, backend=backend)
+    # the layout check also guards the in-place new-token write
+    qkv = torch.randn(B, (Hq + 2 * Hkv) * D).to(torch.float16)
+    cos = torch.ones(16, D // 2)
+    sin = torch.zeros(16, D // 2)
+    for what, bad in cases.items():
+        if what == "Hkv":
+            continue  # original_page_shape check of the update names (Hkv, D) itself
+        with pytest.raises(ValueError):
+            pq.paged_quantized_kv_update_from_qkv(qkv, bad, cos, sin, [0, 1], num_attention_heads=Hq,
+                                                  num_key_value_heads=Hkv, head_dim=D)
+    # a cache tagged with the other bit width is caught too
+    with pytest.raises(ValueError):
+        pq.paged_quantized_kv_gqa_decode_attention(q, dataclasses.replace(c, bits=other), backend=f"metal_q{other}")
+
+
 def test_q4_packed_shape_odd_d():
     Kp = torch.randn(2, 4, 2, 17).to(torch.float16)
     cfg = pq.PagedQuantizedKVConfig(bits=4, page_size=4, group_size=32)
