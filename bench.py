@@ -291,7 +291,8 @@ def decode_stack_config5(dev, batches=(1, 32), steps=128, ctx=2048):
     gen = torch.Generator(device=dev)
     gen.manual_seed(9)
     for B in batches:
-        cache = ls.init_llama_stack_cache(cfg, B, ctx + steps + 2, dtype=torch.float16, page_size=16, device=dev)
+        cache = ls.init_llama_stack_cache(cfg, B, ctx + steps + 2, cache_layout="paged", dtype=torch.float16,
+                                          page_size=16, device=dev)
         for K, V, _ in cache.layer_caches:
             K.normal_(generator=gen)
             V.normal_(generator=gen)

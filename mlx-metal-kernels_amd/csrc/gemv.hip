@@ -71,16 +71,17 @@ __device__ __forceinline__ u32x4 xperm(u32x4 X) {
 }
 
 // Per-group dequant parameters.  The integer part zi of the zero point is
-// subtracted exactly from the magic-biased codes ((1024 + c) - (1024 + zi) =
-// c - zi, exact in fp16 for |zi| < 64 (q4 high nibbles: 16 zi) / 1024 (q8)),
-// so w = fma(c - zi, s, corr) with corr = -(z - zi) s rounds once, to the
-// fp16 of (c - z) s whenever z is an integer -- the rounding of the
-// reference's fp32 dequant -- and keeps a fractional z exact to ulp(corr).
+// subtracted exactly from the magic-biased codes: (1024 + c) - (1024 + zi)
+// for codes at mantissa bits 0..3 (q8: 0..7) of 1024.0h, (64 + c) - (64 + zi)
+// for q4 codes left in place at bits 4..7 under 64.0h (ulp 1/16) -- c - zi
+// exactly in fp16 for |zi| < 1024 -- so w = fma(c - zi, s, corr) with
+// corr = -(z - zi) s rounds once, to the fp16 of (c - z) s whenever z is an
+// integer (the rounding of the reference's fp32 dequant, for any fp16 scale),
+// and keeps a fractional z exact to ulp(corr).
 struct GpMagic {
   f16x2 s;     // (s, s)
-  f16x2 s16;   // (s/16, s/16)  for codes sitting at nibble bits 4..7
   f16x2 kz;    // (1024 + zi)
-  f16x2 kz16;  // (1024 + 16 zi)
+  f16x2 kz64;  // (64 + zi)
   f16x2 corr;  // -(z - zi) * s
 };
 struct GpExact {
@@ -95,25 +96,25 @@ __device__ __forceinline__ GpMagic make_gp_magic(f16 s, f16 z) {
   const float zf = (float)z;
   const float zi = rintf(zf);
   g.s = h2(s);
-  g.s16 = h2(s * (f16)0.0625f);
   g.kz = h2((f16)(1024.0f + zi));
-  g.kz16 = h2((f16)(1024.0f + 16.0f * zi));
+  g.kz64 = h2((f16)(64.0f + zi));
   g.corr = h2((f16)(-(zf - zi) * (float)s));
   return g;
 }
 
 // q4 word (8 codes) -> 8 fp16 weights in order [0,4,1,5,2,6,3,7].
-// `magic` = 0x64006400 held in a VGPR so each unpack is one v_and_or_b32.
-__device__ __forceinline__ u32x4 dq4_magic(uint32_t u, const GpMagic& g, uint32_t magic) {
+// `magic` = 0x64006400 (1024.0h pair) and `magic_hi` = 0x54005400 (64.0h
+// pair) held in VGPRs so each unpack is one v_and_or_b32.
+__device__ __forceinline__ u32x4 dq4_magic(uint32_t u, const GpMagic& g, uint32_t magic, uint32_t magic_hi) {
   const uint32_t v = u >> 8;
-  f16x2 a = bitcast<f16x2>((u & 0x000F000Fu) | magic) - g.kz;    // c0 - zi, c4 - zi
-  f16x2 b = bitcast<f16x2>((u & 0x00F000F0u) | magic) - g.kz16;  // 16 (c1 - zi), 16 (c5 - zi)
-  f16x2 c = bitcast<f16x2>((v & 0x000F000Fu) | magic) - g.kz;    // c2, c6
-  f16x2 d = bitcast<f16x2>((v & 0x00F000F0u) | magic) - g.kz16;  // 16 c3, 16 c7
+  f16x2 a = bitcast<f16x2>((u & 0x000F000Fu) | magic) - g.kz;       // c0 - zi, c4 - zi
+  f16x2 b = bitcast<f16x2>((u & 0x00F000F0u) | magic_hi) - g.kz64;  // c1 - zi, c5 - zi
+  f16x2 c = bitcast<f16x2>((v & 0x000F000Fu) | magic) - g.kz;       // c2, c6
+  f16x2 d = bitcast<f16x2>((v & 0x00F000F0u) | magic_hi) - g.kz64;  // c3, c7
   a = __builtin_elementwise_fma(a, g.s, g.corr);
-  b = __builtin_elementwise_fma(b, g.s16, g.corr);
+  b = __builtin_elementwise_fma(b, g.s, g.corr);
   c = __builtin_elementwise_fma(c, g.s, g.corr);
-  d = __builtin_elementwise_fma(d, g.s16, g.corr);
+  d = __builtin_elementwise_fma(d, g.s, g.corr);
   u32x4 r;
   r[0] = bitcast<uint32_t>(a);
   r[1] = bitcast<uint32_t>(b);
@@ -393,6 +394,7 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(const GemvArgs args) {
   const int m = lane & 15;
   const bool x_active = m < M;
   const uint32_t magic = in_vgpr(BITS == 4 ? 0x64006400u : 0x64646464u);
+  const uint32_t magic_hi = in_vgpr(0x54005400u);  // q4 odd nibbles under 64.0h
 
   // this wave's chunk range
   const int chunks = (K + F::KC - 1) / F::KC;
@@ -467,7 +469,7 @@ __global__ __launch_bounds__(512) void gemv_mfma_kernel(const GemvArgs args) {
 #pragma unroll
           for (int s = j * SPG; s < (j + 1) * SPG; ++s) {
             u32x4 a;
-            if constexpr (BITS == 4) a = dq4_magic(cur.w[t][s >> 2][s & 3], gp, magic);
+            if constexpr (BITS == 4) a = dq4_magic(cur.w[t][s >> 2][s & 3], gp, magic, magic_hi);
             else a = dq8_magic(cur.w[t][s >> 1][(2 * s) & 3], cur.w[t][s >> 1][(2 * s + 1) & 3], gp, magic);
             acc[t] = mfma_k32<AT>(a, xperm<BITS, MAGIC>(xv[s]), acc[t]);
           }
@@ -563,6 +565,7 @@ __global__ __launch_bounds__(NMAT == 1 && BITS == 4 ? 1024 : 512) void gemv_tile
   const int kb = lane >> 4;
   const int n_ld = n0 + r < N ? n0 + r : N - 1;  // rows past N load a valid row; results dropped
   const uint32_t magic = in_vgpr(BITS == 4 ? 0x64006400u : 0x64646464u);
+  const uint32_t magic_hi = in_vgpr(0x54005400u);  // q4 odd nibbles under 64.0h
   const bool has_z = args.z[0] != nullptr;
 
   const int chunks = K >> 7;
@@ -630,7 +633,7 @@ __global__ __launch_bounds__(NMAT == 1 && BITS == 4 ? 1024 : 512) void gemv_tile
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         u32x4 a;
-        if constexpr (BITS == 4) a = dq4_magic(b.w[t][0][s], gp, magic);
+        if constexpr (BITS == 4) a = dq4_magic(b.w[t][0][s], gp, magic, magic_hi);
         else a = dq8_magic(b.w[t][s >> 1][(2 * s) & 3], b.w[t][s >> 1][(2 * s + 1) & 3], gp, magic);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mfma_k32<f16>(a, xp[mt][s], acc[t][mt]);

@@ -140,21 +140,22 @@ __device__ __forceinline__ u32x4 deq8x8(uint32_t u0, uint32_t u1, f16x2 s2) {
   r[3] = q8_pair(u1, 8, s2);
   return r;
 }
-// 8 q4 codes (one word) -> 8 fp16, order [0,4,1,5,2,6,3,7].  Odd nibbles
-// stay in place: (1024 + 16 c) - (1024 + 128) = 16 (c - 8) exactly, times
-// s / 16 -- the same product (c - 8) s whenever s / 16 is a normal fp16
-// (s >= 2^-10), one shift per word instead of three.
+// 8 q4 codes (one word) -> 8 fp16, order [0,4,1,5,2,6,3,7].  Even nibbles
+// sit at mantissa bits 0..3 of 1024.0h (ulp 1): 1024 + c.  Odd nibbles stay
+// in place at bits 4..7 under the exponent of 64.0h (ulp 1/16): 64 + c.  So
+// both halves give (c - 8) exactly after one subtraction and share the same
+// scale multiply, which rounds (c - 8) * s once -- one shift per word.
 __device__ __forceinline__ u32x4 deq4x8(uint32_t u, f16x2 s2) {
   const f16x2 k_lo = {(f16)1032.0f, (f16)1032.0f};  // 1024 + 8
-  const f16x2 k_hi = {(f16)1152.0f, (f16)1152.0f};  // 1024 + 16 * 8
-  const f16x2 s16 = s2 * (f16x2){(f16)0.0625f, (f16)0.0625f};
-  const uint32_t magic = 0x64006400u;
+  const f16x2 k_hi = {(f16)72.0f, (f16)72.0f};      // 64 + 8
+  const uint32_t magic_lo = 0x64006400u;            // 1024.0h
+  const uint32_t magic_hi = 0x54005400u;            // 64.0h
   const uint32_t v = u >> 8;
   u32x4 r;
-  r[0] = bitcast<uint32_t>((bitcast<f16x2>((u & 0x000F000Fu) | magic) - k_lo) * s2);
-  r[1] = bitcast<uint32_t>((bitcast<f16x2>((u & 0x00F000F0u) | magic) - k_hi) * s16);
-  r[2] = bitcast<uint32_t>((bitcast<f16x2>((v & 0x000F000Fu) | magic) - k_lo) * s2);
-  r[3] = bitcast<uint32_t>((bitcast<f16x2>((v & 0x00F000F0u) | magic) - k_hi) * s16);
+  r[0] = bitcast<uint32_t>((bitcast<f16x2>((u & 0x000F000Fu) | magic_lo) - k_lo) * s2);
+  r[1] = bitcast<uint32_t>((bitcast<f16x2>((u & 0x00F000F0u) | magic_hi) - k_hi) * s2);
+  r[2] = bitcast<uint32_t>((bitcast<f16x2>((v & 0x000F000Fu) | magic_lo) - k_lo) * s2);
+  r[3] = bitcast<uint32_t>((bitcast<f16x2>((v & 0x00F000F0u) | magic_hi) - k_hi) * s2);
   return r;
 }
 
@@ -243,14 +244,12 @@ __device__ __forceinline__ u32x2 deq8x4(uint32_t u, f16x2 s2) {
 }
 __device__ __forceinline__ u32x2 deq4x4(uint32_t u, f16x2 s2) {
   // bytes (b0, 0, b1, 0): n0 n1 @ bits 0..7, n2 n3 @ 16..23, one v_perm_b32;
-  // the odd nibbles stay in place against s / 16 as in deq4x8
+  // the odd nibbles stay in place under 64.0h as in deq4x8
   const uint32_t t = perm_b32(0u, u, 0x04010400u);
   const f16x2 k_lo = {(f16)1032.0f, (f16)1032.0f};
-  const f16x2 k_hi = {(f16)1152.0f, (f16)1152.0f};
-  const f16x2 s16 = s2 * (f16x2){(f16)0.0625f, (f16)0.0625f};
-  const uint32_t magic = 0x64006400u;
-  return (u32x2){bitcast<uint32_t>((bitcast<f16x2>((t & 0x000F000Fu) | magic) - k_lo) * s2),
-                 bitcast<uint32_t>((bitcast<f16x2>((t & 0x00F000F0u) | magic) - k_hi) * s16)};
+  const f16x2 k_hi = {(f16)72.0f, (f16)72.0f};
+  return (u32x2){bitcast<uint32_t>((bitcast<f16x2>((t & 0x000F000Fu) | 0x64006400u) - k_lo) * s2),
+                 bitcast<uint32_t>((bitcast<f16x2>((t & 0x00F000F0u) | 0x54005400u) - k_hi) * s2)};
 }
 
 __device__ __forceinline__ f16x2 splat_h(uint32_t s) {
@@ -1364,6 +1363,36 @@ int attention_launch(PagedArgs a, int64_t D, int kvf, int dtype, size_t ws_bytes
   return MK_OK;
 }
 
+// Argument checks and PagedArgs set-up shared by the fp16/bf16 entry points.
+int fp16_args(PagedArgs& a, const void* q, const void* K_pages, const void* V_pages,
+              const int32_t* block_table, const int32_t* lengths, void* out, int64_t B,
+              int64_t Hq, int64_t Hkv, int64_t D, int64_t page_size, int64_t max_blocks,
+              int64_t num_pages, float scale, int dtype) {
+  MK_REQUIRE(q && K_pages && V_pages && block_table && lengths && out);
+  MK_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && (Hq % Hkv) == 0 && D > 0 && page_size > 0);
+  MK_REQUIRE(max_blocks > 0 && num_pages > 0 && num_pages < (1LL << 31));
+  MK_REQUIRE(B < 65536 && max_blocks * page_size < (1LL << 31));
+  MK_REQUIRE(dtype == MK_DT_F16 || dtype == MK_DT_BF16);
+  a.q = q;
+  a.K = K_pages;
+  a.V = V_pages;
+  a.bt = block_table;
+  a.lengths = lengths;
+  a.out = out;
+  a.B = (int)B;
+  a.Hq = (int)Hq;
+  a.Hkv = (int)Hkv;
+  a.G = (int)(Hq / Hkv);
+  a.HB = (a.G + 15) / 16;
+  a.NP = (int)num_pages;
+  a.P = (int)page_size;
+  a.MB = (int)max_blocks;
+  a.gs = 1;
+  a.ngroups = 1;
+  a.scale_log2 = scale * kLog2e;
+  return MK_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1390,31 +1419,11 @@ int mk_paged_decode_attention(const void* q, const void* K_pages, const void* V_
                               int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t page_size,
                               int64_t max_blocks, int64_t num_pages, float scale, int dtype,
                               void* workspace, size_t workspace_bytes, void* stream) {
-  MK_REQUIRE(q && K_pages && V_pages && block_table && lengths && out);
-  MK_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && (Hq % Hkv) == 0 && D > 0 && page_size > 0);
-  MK_REQUIRE(max_blocks > 0 && num_pages > 0 && num_pages < (1LL << 31));
-  MK_REQUIRE(B < 65536 && max_blocks * page_size < (1LL << 31));
-  MK_REQUIRE(dtype == MK_DT_F16 || dtype == MK_DT_BF16);
-  if (B == 0) return MK_OK;
   PagedArgs a = {};
-  a.q = q;
-  a.K = K_pages;
-  a.V = V_pages;
-  a.bt = block_table;
-  a.lengths = lengths;
-  a.out = out;
+  const int rc = fp16_args(a, q, K_pages, V_pages, block_table, lengths, out, B, Hq, Hkv, D,
+                           page_size, max_blocks, num_pages, scale, dtype);
+  if (rc != MK_OK || B == 0) return rc;
   a.ws = reinterpret_cast<float*>(workspace);
-  a.B = (int)B;
-  a.Hq = (int)Hq;
-  a.Hkv = (int)Hkv;
-  a.G = (int)(Hq / Hkv);
-  a.HB = (a.G + 15) / 16;
-  a.NP = (int)num_pages;
-  a.P = (int)page_size;
-  a.MB = (int)max_blocks;
-  a.gs = 1;
-  a.ngroups = 1;
-  a.scale_log2 = scale * kLog2e;
   return attention_launch(a, D, 0, dtype, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 

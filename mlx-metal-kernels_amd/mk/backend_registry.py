@@ -16,6 +16,26 @@ from __future__ import annotations
 from copy import deepcopy
 
 BACKEND_REGISTRY = {
+    "decode_attention": {
+        "function": "mk.decode_ops.decode_attention",
+        "reference_backend": "reference",
+        "candidate_backends": ["metal", "metal_threadgroup", "metal_d64", "metal_d128"],
+    },
+    "quantized_kv_decode_attention": {
+        "function": "mk.quantized_kv_cache_ops.quantized_kv_gqa_decode_attention",
+        "reference_backend": "reference",
+        "candidate_backends": ["metal_q8", "metal_q4"],
+    },
+    "llama_layer_decode": {
+        "function": "mk.llama_layer_ops.llama_layer_decode_loop",
+        "reference_backend": "reference",
+        "candidate_backends": ["metal", "tiled", "fused_experimental"],
+    },
+    "llama_stack_decode": {
+        "function": "mk.llama_stack_ops.llama_stack_decode_loop",
+        "reference_backend": "reference",
+        "candidate_backends": ["metal", "tiled", "fused_experimental"],
+    },
     "paged_decode_attention": {
         "function": "mk.paged_kv_ops.paged_decode_attention",
         "reference_backend": "reference",
@@ -118,9 +138,15 @@ def _keep(op_name: str, backend: str, shape: dict, dtype_name: str) -> bool:
         return False
     if op_name == "quantized_mlp_block" and backend == "fused_experimental":
         return shape.get("bits") in (4, 8) and dtype_name == "float16"
+    if op_name in ("llama_layer_decode", "llama_stack_decode"):
+        # the reference also drops every backend of a paged stack (it has
+        # none); the paged stack runs here, so that rule is not kept
+        if shape.get("bits") not in (4, 8):
+            return False
+        return backend != "fused_experimental" or dtype_name == "float16"
     if op_name == "paged_gqa_decode_attention" and backend != "reference":
         return _gqa_heads_ok(shape)
-    if op_name == "paged_quantized_kv_decode_attention" and backend != "reference":
+    if op_name in ("paged_quantized_kv_decode_attention", "quantized_kv_decode_attention") and backend != "reference":
         bits = shape.get("bits")
         if not _gqa_heads_ok(shape):
             return False

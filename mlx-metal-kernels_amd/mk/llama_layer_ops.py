@@ -21,6 +21,7 @@ from typing import Any
 
 import torch
 
+from . import _contig
 from .mlp_block_ops import quantized_mlp_block, reference_quantized_mlp_block
 from .norm_ops import reference_rms_norm, rms_norm
 from .quantized_decode_block_ops import paged_quantized_decode_block, reference_paged_quantized_decode_block
@@ -167,27 +168,48 @@ def _zero_residual(h):
 
 
 def _check_decode(x, config: LlamaLikeConfig, cache, cache_layout: str):
+    """(K_pages, V_pages, block_table, restore) for either cache layout.
+
+    "paged": cache = (K_pages, V_pages, block_table).  "contiguous" (the
+    reference's default, ops/llama_layer_ops.py:251-255): cache = (K_cache,
+    V_cache) [B, MAX_S, Hkv, D], served as an identity-paged view of the same
+    memory; ``restore`` turns the (possibly new) page tensors back into the
+    caller's layout."""
     if x.ndim != 3 or x.shape[1] != 1 or x.shape[2] != config.hidden_size:
         raise ValueError(f"x must have shape [B,1,{config.hidden_size}], got {tuple(x.shape)}")
-    if cache_layout != "paged":
-        raise ValueError("this build implements the paged cache layout (cache_layout='paged'); "
-                         f"got {cache_layout!r}")
-    if not isinstance(cache, tuple) or len(cache) != 3:
-        raise ValueError("paged cache must be a tuple (K_pages, V_pages, block_table)")
-    return cache
+    if cache_layout == "paged":
+        if not isinstance(cache, tuple) or len(cache) != 3:
+            raise ValueError("paged cache must be a tuple (K_pages, V_pages, block_table)")
+        return cache + ((lambda K, V, bt: (K, V, bt)),)
+    if cache_layout != "contiguous":
+        raise ValueError(f"cache_layout must be one of ('contiguous', 'paged'), got {cache_layout!r}")
+    if not isinstance(cache, tuple) or len(cache) != 2:
+        raise ValueError("contiguous cache must be a tuple (K_cache, V_cache)")
+    K_cache, V_cache = cache
+    want = (x.shape[0], K_cache.shape[1] if K_cache.ndim == 4 else -1, config.num_key_value_heads, config.head_dim)
+    if K_cache.ndim != 4 or tuple(K_cache.shape) != want or K_cache.shape != V_cache.shape:
+        raise ValueError(f"K_cache and V_cache must have shape [B,MAX_S,Hkv,D]={want}, got "
+                         f"{tuple(K_cache.shape)}, {tuple(V_cache.shape)}")
+    B, S = K_cache.shape[:2]
+    P = _contig.page_size_for(S)
+    bt = _contig.identity_table(B, S, P, K_cache.device)
+    shape = tuple(K_cache.shape)
+    return (_contig.as_pages(K_cache, P), _contig.as_pages(V_cache, P), bt,
+            (lambda K, V, _bt: (K.reshape(shape), V.reshape(shape))))
 
 
 def llama_layer_decode_step(x, weights: LlamaLayerKernelWeights, cache, cos, sin, position, config,
-                            *, cache_layout: str = "paged", return_intermediates: bool = False, lengths=None):
-    """ops/llama_layer_ops.py:234-428, paged layout, all stages on HIP.
-    x [B,1,hidden]; cache (K_pages, V_pages, block_table) updated in place;
+                            *, cache_layout: str = "contiguous", return_intermediates: bool = False, lengths=None):
+    """ops/llama_layer_ops.py:234-428, all stages on HIP.  x [B,1,hidden];
+    cache (K_pages, V_pages, block_table) for cache_layout="paged" or
+    (K_cache, V_cache) [B,MAX_S,Hkv,D] for "contiguous", updated in place;
     position int or per-sequence [B].  Returns (out, cache) or
     (out, cache, intermediates).  The input RMSNorm runs inside the qkv
     matvec and the residual add inside the o-proj matvec; ``lengths``
     (extension) = position + 1 as a device tensor shared by all layers."""
     config = config.validate()
     weights.validate(config)
-    K_pages, V_pages, block_table = _check_decode(x, config, cache, cache_layout)
+    K_pages, V_pages, block_table, restore = _check_decode(x, config, cache, cache_layout)
     # without intermediates the norm, qkv projection, RoPE and cache write are
     # one launch (the projection is then never materialised)
     blk = paged_quantized_decode_block(
@@ -203,7 +225,7 @@ def llama_layer_decode_step(x, weights: LlamaLayerKernelWeights, cache, cos, sin
                               gate_zeros=weights.gate_zeros, up_zeros=weights.up_zeros, down_zeros=weights.down_zeros,
                               bits=weights.bits, group_size=weights.group_size, eps=config.rms_norm_eps,
                               backend_preset="fused_experimental", return_intermediates=return_intermediates)
-    cache = (K_pages, V_pages, block_table)
+    cache = restore(K_pages, V_pages, block_table)
     if not return_intermediates:
         return res, cache
     out, mi = res
@@ -213,12 +235,12 @@ def llama_layer_decode_step(x, weights: LlamaLayerKernelWeights, cache, cos, sin
 
 
 def reference_llama_layer_decode_step(x, weights: LlamaLayerKernelWeights, cache, cos, sin, position, config,
-                                      *, cache_layout: str = "paged", return_intermediates: bool = False):
+                                      *, cache_layout: str = "contiguous", return_intermediates: bool = False):
     """ops/llama_layer_ops.py:214-231 (every stage on the torch reference
     path; the cache is updated functionally, the input cache untouched)."""
     config = config.validate()
     weights.validate(config)
-    K_pages, V_pages, block_table = _check_decode(x, config, cache, cache_layout)
+    K_pages, V_pages, block_table, restore = _check_decode(x, config, cache, cache_layout)
     x_norm = reference_rms_norm(x, weights.input_layernorm_weight, eps=config.rms_norm_eps)
     attn_proj, K_pages, V_pages, qkv, attn_out = reference_paged_quantized_decode_block(
         x_norm, weights.qkv_w, weights.qkv_scales, weights.o_w, weights.o_scales, K_pages, V_pages, block_table, cos,
@@ -232,12 +254,54 @@ def reference_llama_layer_decode_step(x, weights: LlamaLayerKernelWeights, cache
                                         down_zeros=weights.down_zeros, bits=weights.bits,
                                         group_size=weights.group_size, eps=config.rms_norm_eps,
                                         return_intermediates=return_intermediates)
-    cache = (K_pages, V_pages, block_table)
+    cache = restore(K_pages, V_pages, block_table)
     if not return_intermediates:
         return res, cache
     out, mi = res
     return out, cache, {"x_norm": x_norm, "qkv": qkv, "attn_out": attn_out, "h": h, "mlp_norm": mi["normed"],
                         "gate": mi["gate"], "up": mi["up"], "mlp": mi["mlp"], "down": mi["down"]}
+
+
+_LOOP_PRESETS = ("reference", "metal", "tiled", "fused_experimental")
+
+
+def llama_layer_decode_loop(inputs, weights: LlamaLayerKernelWeights, cache, cos, sin, config, *,
+                            backend_preset: str = "fused_experimental", cache_layout: str = "contiguous",
+                            T: int | None = None, return_final_cache: bool = True):
+    """ops/llama_layer_ops.py:431-467: decode inputs [B, T, hidden] one step
+    at a time, step t at position t of every sequence.  Preset "reference"
+    runs every stage on the torch reference path (functional cache updates);
+    the other presets run the HIP layer (caches updated in place).  Returns
+    (out [B, T, hidden], final cache) or out alone."""
+    if inputs.ndim != 3:
+        raise ValueError(f"inputs must have shape [B,T,hidden_size], got {tuple(inputs.shape)}")
+    if backend_preset not in _LOOP_PRESETS:
+        raise ValueError(f"backend_preset must be one of {_LOOP_PRESETS}, got {backend_preset}")
+    T = inputs.shape[1] if T is None else T
+    step = reference_llama_layer_decode_step if backend_preset == "reference" else llama_layer_decode_step
+    outputs = []
+    running = cache
+    for t in range(T):
+        out_t, running = step(inputs[:, t:t + 1, :], weights, running, cos, sin, t, config, cache_layout=cache_layout)
+        outputs.append(out_t)
+    out = torch.cat(outputs, dim=1) if len(outputs) > 1 else outputs[0]
+    return (out, running) if return_final_cache else out
+
+
+def init_llama_layer_cache(config: LlamaLikeConfig, B: int, max_seq_len: int, *, cache_layout: str = "contiguous",
+                           dtype=torch.float16, page_size: int = 16, device=None):
+    """ops/llama_layer_ops.py:516-526: zero (K_cache, V_cache) [B, MAX_S, Hkv, D]
+    or the paged (K_pages, V_pages, identity block table)."""
+    from .paged_kv_ops import allocate_paged_kv_cache
+
+    config = config.validate()
+    if cache_layout == "contiguous":
+        shape = (B, max_seq_len, config.num_key_value_heads, config.head_dim)
+        return (torch.zeros(shape, dtype=dtype, device=device), torch.zeros(shape, dtype=dtype, device=device))
+    if cache_layout == "paged":
+        return allocate_paged_kv_cache(B, max_seq_len, config.num_key_value_heads, config.head_dim, page_size, dtype,
+                                       device=device)
+    raise ValueError(f"cache_layout must be 'contiguous' or 'paged', got {cache_layout}")
 
 
 def kv_pages_for(config: LlamaLikeConfig, B: int, max_seq_len: int, page_size: int = 16):

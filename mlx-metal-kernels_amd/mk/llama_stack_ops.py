@@ -91,14 +91,21 @@ class LlamaStackCache:
         return len(self.layer_caches)
 
 
-def init_llama_stack_cache(config: LlamaLikeConfig, B: int, max_seq_len: int, *, cache_layout: str = "paged",
+def init_llama_stack_cache(config: LlamaLikeConfig, B: int, max_seq_len: int, *, cache_layout: str = "contiguous",
                            dtype=torch.float16, page_size: int = 16, device=None, block_table=None):
-    """ops/llama_stack_ops.py:195-221 for the paged layout: per layer
-    K/V pages [B * ceil(max_seq_len / P), P, Hkv, D] (zeros) sharing one
-    block table [B, ceil(max_seq_len / P)] (identity unless given)."""
+    """ops/llama_stack_ops.py:195-221.  "contiguous": per layer zero
+    (K_cache, V_cache) [B, max_seq_len, Hkv, D].  "paged" (which the
+    reference leaves unimplemented): per layer K/V pages
+    [B * ceil(max_seq_len / P), P, Hkv, D] (zeros) sharing one block table
+    [B, ceil(max_seq_len / P)] (identity unless given)."""
     config = config.validate()
+    if cache_layout == "contiguous":
+        shape = (B, max_seq_len, config.num_key_value_heads, config.head_dim)
+        caches = [(torch.zeros(shape, dtype=dtype, device=device), torch.zeros(shape, dtype=dtype, device=device))
+                  for _ in range(config.num_hidden_layers)]
+        return LlamaStackCache(caches, "contiguous", max_seq_len, None)
     if cache_layout != "paged":
-        raise ValueError(f"this build implements the paged cache layout, got {cache_layout!r}")
+        raise ValueError(f"cache_layout must be one of ('contiguous', 'paged'), got {cache_layout!r}")
     mb = math.ceil(max_seq_len / page_size)
     if block_table is None:
         block_table = torch.arange(B * mb, dtype=torch.int32, device=device).reshape(B, mb)
@@ -165,14 +172,14 @@ def llama_stack_decode_step(x, stack_weights: LlamaStackWeights, stack_cache: Ll
     for li, lw in enumerate(stack_weights.layers):
         if reference:
             hidden, cache = reference_llama_layer_decode_step(hidden, lw, stack_cache.layer_caches[li], cos, sin,
-                                                              position, config)
+                                                              position, config, cache_layout=stack_cache.cache_layout)
         else:
             hidden, cache = llama_layer_decode_step(hidden, lw, stack_cache.layer_caches[li], cos, sin, position,
-                                                    config, lengths=lengths)
+                                                    config, cache_layout=stack_cache.cache_layout, lengths=lengths)
         new_caches.append(cache)
         if return_intermediates:
             layers_out.append(hidden)
-    cache = LlamaStackCache(new_caches, "paged", stack_cache.max_seq_len, stack_cache.page_size)
+    cache = LlamaStackCache(new_caches, stack_cache.cache_layout, stack_cache.max_seq_len, stack_cache.page_size)
     head = stack_weights.lm_head
     logits = None
     if isinstance(head, QuantizedHead) and not reference:
@@ -195,6 +202,51 @@ def llama_stack_decode_step(x, stack_weights: LlamaStackWeights, stack_cache: Ll
         inter["logits"] = logits
         return logits, final_hidden, cache, inter
     return logits, final_hidden, cache
+
+
+def llama_stack_decode_loop(inputs, stack_weights: LlamaStackWeights, stack_cache: LlamaStackCache, cos, sin,
+                            config: LlamaLikeConfig, *, backend_preset: str = "fused_experimental",
+                            cache_layout: str = "contiguous", T: int | None = None, return_logits: bool = True):
+    """ops/llama_stack_ops.py:439-495: decode inputs [B, T, hidden] (or
+    [B, T, 1, hidden]) one step at a time, step t at position t of every
+    sequence.  Returns (logits [B, T, vocab] -- or the final hidden states
+    when ``return_logits`` is False or there is no head -- and the final
+    cache).  Preset "reference" runs the torch reference path."""
+    if inputs.ndim == 4:
+        if inputs.shape[2] != 1:
+            raise ValueError(f"inputs with rank 4 must have shape [B,T,1,H], got {tuple(inputs.shape)}")
+        inputs = inputs[:, :, 0, :]
+    if inputs.ndim != 3:
+        raise ValueError(f"inputs must have shape [B,T,H] or [B,T,1,H], got {tuple(inputs.shape)}")
+    if backend_preset not in ("reference", "metal", "tiled", "fused_experimental"):
+        raise ValueError("layer_backend_preset must be one of ('reference', 'metal', 'tiled', 'fused_experimental')")
+    if cache_layout not in ("contiguous", "paged"):
+        raise ValueError("cache_layout must be one of ('contiguous', 'paged')")
+    if cache_layout != stack_cache.cache_layout:
+        raise ValueError(f"cache_layout {cache_layout!r} does not match the stack cache's "
+                         f"{stack_cache.cache_layout!r}")
+    T = inputs.shape[1] if T is None else T
+    outputs = []
+    running = stack_cache
+    for t in range(T):
+        result = llama_stack_decode_step(inputs[:, t:t + 1, :], stack_weights, running, cos, sin, t, config,
+                                         reference=backend_preset == "reference")
+        if stack_weights.lm_head is None:
+            out_t, running = result
+        else:
+            logits_t, final_hidden_t, running = result
+            out_t = logits_t if return_logits else final_hidden_t
+        outputs.append(out_t)
+    out = torch.cat(outputs, dim=1) if len(outputs) > 1 else outputs[0]
+    return out, running
+
+
+def reference_llama_stack_decode_loop(inputs, stack_weights: LlamaStackWeights, stack_cache: LlamaStackCache, cos,
+                                      sin, config: LlamaLikeConfig, *, cache_layout: str = "contiguous",
+                                      T: int | None = None, return_logits: bool = True):
+    """ops/llama_stack_ops.py:413-436."""
+    return llama_stack_decode_loop(inputs, stack_weights, stack_cache, cos, sin, config, backend_preset="reference",
+                                   cache_layout=cache_layout, T=T, return_logits=return_logits)
 
 
 def _random_linear(out_dim, in_dim, bits, group_size, gen, device, dtype):
@@ -247,7 +299,14 @@ class DecodeGraph:
     """One greedy decode step captured in a HIP graph: token ids [B] (int64,
     device) at per-sequence positions [B] (int32, device) -> next token ids,
     with every layer's cache written at those positions.  ``step()`` replays
-    the graph and advances the positions by one in place."""
+    the graph and advances the positions by one in place.
+
+    Construction already performs the first decode step, eagerly (it warms
+    every buffer the capture reuses): the caches hold the given tokens at the
+    given positions, ``first_tokens`` holds that step's output, ``tokens`` is
+    the input of the first ``step()`` (equal to ``first_tokens``) and
+    ``positions`` has advanced by one.  So the tokens of a greedy run are
+    ``first_tokens`` followed by the output of each ``step()``."""
 
     def __init__(self, stack_weights: LlamaStackWeights, stack_cache: LlamaStackCache, cos, sin,
                  config: LlamaLikeConfig, token_ids, positions):
@@ -259,7 +318,7 @@ class DecodeGraph:
         self.stream = torch.cuda.Stream(device=self.tokens.device)
         self.stream.wait_stream(torch.cuda.current_stream(self.tokens.device))
         with torch.cuda.stream(self.stream):
-            self._run()  # warm every cached buffer outside the capture
+            self.first_tokens = self._run().clone()  # the first step; warms every buffer outside the capture
         self.stream.synchronize()
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph, stream=self.stream):

@@ -210,3 +210,43 @@ def qkv_rope_paged_update_quant(qkv, cos, sin, pos, bt, kq, vq, ks, vs, Hq, Hkv,
         ks[page[b], off[b]] = ksn[b]
         vs[page[b], off[b]] = vsn[b]
     return q, kq, vq, ks, vs
+
+
+# ----------------------------------------------------------------- contiguous caches
+
+
+def contiguous_update(K, V, k_new, v_new, pos):
+    """ops/kv_cache_ops.py:93-107: functional copy of K/V [B, MAX_S, H, D]
+    with row pos[b] of sequence b replaced by k_new[b] / v_new[b]."""
+    K, V = K.copy(), V.copy()
+    for b, p in enumerate(np.broadcast_to(np.asarray(pos), (K.shape[0],))):
+        K[b, p] = k_new[b]
+        V[b, p] = v_new[b]
+    return K, V
+
+
+def contiguous_attention(q, K, V, lengths, scale=None):
+    """Decode attention over a contiguous cache K/V [B, MAX_S, Hkv, D] at
+    positions j < min(lengths[b], MAX_S): ops/decode_ops.py:93-123 (MHA),
+    ops/gqa_ops.py:278-304 (GQA) and ops/quantized_kv_cache_ops.py:377-406
+    (after dequantization).  float64 [B, Hq, D]."""
+    D = q.shape[-1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    lengths = np.minimum(np.broadcast_to(np.asarray(lengths), (q.shape[0],)), K.shape[1])
+    return attention(q, K, V, lengths, np.ones(K.shape[:2], bool), scale)
+
+
+def quantize_contiguous(K, V, group_size: int, bits: int, lengths=None):
+    """ops/quantized_kv_cache_ops.py:173-277: the quantizer of :131-170 on
+    positions j < lengths[b] (all when None); the other positions keep zero
+    codes and zero scales.  Returns (kq, vq, ks, vs), q4 codes packed."""
+    kq, ks = quantize_groups(K, group_size, bits)
+    vq, vs = quantize_groups(V, group_size, bits)
+    if lengths is not None:
+        keep = np.arange(K.shape[1])[None, :] < np.asarray(lengths).reshape(-1, 1)
+        kq[~keep], vq[~keep] = 0, 0
+        ks[~keep], vs[~keep] = 0, 0
+    if bits == 4:
+        kq, vq = pack_last(kq), pack_last(vq)
+    return kq, vq, ks, vs

@@ -82,7 +82,7 @@ def test_paged_decode_layer_vs_oracle(dev, bits):
     Kt, Vt, btt = (torch.from_numpy(a).to(dev) for a in (K, V, bt))
     out, (K2, V2, _), inter = ll.llama_layer_decode_step(
         torch.from_numpy(x).to(dev)[:, None], _t_layer(lw, dev, bits, g), (Kt, Vt, btt), tc, ts,
-        torch.from_numpy(pos).to(dev), cfg, return_intermediates=True)
+        torch.from_numpy(pos).to(dev), cfg, cache_layout="paged", return_intermediates=True)
     assert_close(out[:, 0], ref, what=f"layer out q{bits}")
     # the new token's k/v, written in place at (bt[b, pos // P], pos % P)
     page, off = op.block_table_lookup(bt, pos, P)
@@ -113,9 +113,10 @@ def test_paged_decode_layer_matches_reference_backend(dev):
     tc, ts = ll.build_rope_tables(cfg, device=dev)
     w = _t_layer(lw, dev, 4, g)
     cache = tuple(torch.from_numpy(a).to(dev) for a in (K, V, bt))
-    ref, (Kr, _, _) = ll.reference_llama_layer_decode_step(x, w, cache, tc, ts, pos, cfg)
+    ref, (Kr, _, _) = ll.reference_llama_layer_decode_step(x, w, cache, tc, ts, pos, cfg, cache_layout="paged")
     assert torch.equal(cache[0].cpu(), torch.from_numpy(K)), "the reference path leaves its input cache alone"
-    out, (K2, _, _) = ll.llama_layer_decode_step(x, w, tuple(t.clone() for t in cache), tc, ts, pos, cfg)
+    out, (K2, _, _) = ll.llama_layer_decode_step(x, w, tuple(t.clone() for t in cache), tc, ts, pos, cfg,
+                                                 cache_layout="paged")
     assert_close(out, ref.float().cpu().numpy(), what="HIP vs reference backend")
     assert_close(K2, Kr.float().cpu().numpy(), what="cache after the step")
 
@@ -155,7 +156,8 @@ def test_decode_stack_greedy_tokens_vs_oracle(dev):
     pos = np.array(ctx, np.int32)
     graph = ls.DecodeGraph(wts, cache, tc, ts, cfg, torch.from_numpy(tokens).to(dev),
                            torch.from_numpy(pos).to(dev))
-    first = graph.tokens.cpu().numpy()  # the construction's eager step
+    first = graph.first_tokens.cpu().numpy()  # the construction's eager step
+    assert np.array_equal(first, graph.tokens.cpu().numpy())
     hip_steps = [first] + [graph.step().cpu().numpy() for _ in range(3)]
     oc = caches_np
     cur = tokens
@@ -181,14 +183,17 @@ def test_fused_norm_qkv_rope_paged_matches_two_step(dev, bits, B):
     writes -- against the separate norm + projection + update ops on the same
     inputs: q and every cache byte equal.  From B = 3 on, rows 1 and 2 target
     one slot (the later row wins)."""
+    rng = np.random.default_rng(90 + bits + B)
+    cfg, g, P, mb = _cfg(1), 32, 16, 4
+    fused_vs_two_step(dev, rng, cfg, _t_layer(_np_layer(rng, cfg, bits, g), dev, bits, g), bits, B, g, P, mb)
+
+
+def fused_vs_two_step(dev, rng, cfg, w, bits, B, g, P, mb):
+    from mk import _lib
     from mk import gqa_ops
     from mk import quantized_decode_block_ops as qd
     from mk.quant_ops import q_rmsnorm_matvec
 
-    rng = np.random.default_rng(90 + bits + B)
-    cfg, g, P, mb = _cfg(1), 32, 16, 4
-    lw = _np_layer(rng, cfg, bits, g)
-    w = _t_layer(lw, dev, bits, g)
     Hq, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
     K0, V0, bt = _caches(rng, B, mb, P, Hkv, D, 1.0)
     pos = rng.integers(0, mb * P, size=B).astype(np.int32)
@@ -208,7 +213,6 @@ def test_fused_norm_qkv_rope_paged_matches_two_step(dev, bits, B):
                            group_size=g)
     x_, c_, s_, p_, q_ref, _ = gqa_ops._qkv_rope_update_prep(qkv[:, None], btt, tc, ts, post, Hq, Hkv, D, P,
                                                              torch.float16, dev)
-    from mk import _lib
     _lib.launch("mk_qkv_rope_paged_update", dev, _lib.ptr(x_), _lib.ptr(c_), _lib.ptr(s_), _lib.ptr(p_),
                 _lib.ptr(btt), _lib.ptr(Kr), _lib.ptr(Vr), _lib.ptr(q_ref), B, Hq, Hkv, D, P, mb, Kr.shape[0],
                 c_.shape[0], _lib.DT_F16)

@@ -330,6 +330,73 @@ def test_quantized_attention(dev, bits, B, Hq, Hkv, D, P, mb, g):
 
 
 @pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("D", [128, 64])
+@pytest.mark.parametrize("amp", [1.0, 1e-3])
+def test_quantized_attention_length_one_is_exact_dequant(dev, bits, D, amp):
+    """With one position the softmax weight is exactly 1, so each head's
+    output is its kv head's dequantized V row: (code - 128|8) * s rounded to
+    fp16 once (dequantize_kv_pages, ops/paged_quantized_kv_ops.py:295-341),
+    bit for bit -- also for groups of amplitude 1e-3 (fp16 scales below
+    2^-10).  Then the same small-amplitude cache at full lengths, at
+    tolerance relative to the output's size."""
+    B, Hq, Hkv, P, mb, g = 3, 8, 2, 16, 6, 64
+    q, Kp, Vp, bt, _ = _case(120 + D + bits, B, Hq, Hkv, D, P, mb)
+    K16, V16 = (Kp * amp).astype(np.float16), (Vp * amp).astype(np.float16)
+    kq, vq, ks, vs = op.quantize_pages(K16, V16, g, bits)
+    lengths = np.ones(B, np.int32)
+    cache = pq.PagedQuantizedKVCache(k_pages_q=to_dev(kq, dev), v_pages_q=to_dev(vq, dev), k_scales=to_dev(ks, dev),
+                                     v_scales=to_dev(vs, dev), block_table=to_dev(bt, dev),
+                                     lengths=to_dev(lengths, dev), bits=bits, page_size=P, group_size=g,
+                                     original_page_shape=K16.shape)
+    qt = _t(q, dev, torch.float16)
+    got = pq.paged_quantized_kv_gqa_decode_attention(qt[:, None], cache, backend=f"metal_q{bits}")[:, 0]
+    _, Vd = op.dequantize_pages(kq, vq, ks, vs, g, bits, D)
+    want = np.stack([Vd[bt[b, 0], 0][np.arange(Hq) // (Hq // Hkv)] for b in range(B)])
+    assert np.array_equal(got.cpu().numpy().view(np.uint16), want.view(np.uint16))
+    full = np.full(B, mb * P - 5, np.int32)
+    cache.lengths = to_dev(full, dev)
+    got = pq.paged_quantized_kv_gqa_decode_attention(qt[:, None], cache, backend=f"metal_q{bits}")[:, 0]
+    ref = op.quantized_paged_attention(qt.float().cpu().numpy(), kq, vq, ks, vs, bt, full, g, bits)
+    rms = float(np.sqrt(np.mean(ref * ref)))
+    assert_close(got.float().cpu().numpy() / rms, ref / rms, what=f"q{bits} D{D} amplitude {amp}")
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("D", [128, 64])
+def test_config4_full_context(dev, bits, D):
+    """B = 8 sequences of 32768 positions, 32/8 heads,
+    P = 16, g = 64, q8 / q4 pages quantized on the device (mk_quantize_kv,
+    bit-exact against the oracle's quantizer elsewhere), permuted block table.
+    At this size the stream plan runs pairs at the 32-block cap (q8 at its
+    4-block minimum split) and 32 partials per sequence.  The last sequence
+    stops 77 positions short of the table.  The float64 reference is computed
+    per sequence over that sequence's pages only, to bound host memory."""
+    B, Hq, Hkv, P, g, mb = 8, 32, 8, 16, 64, 2048
+    print(f"config 4 full context q{bits} D{D}", flush=True)
+    NP = B * mb
+    gen = torch.Generator(device=dev).manual_seed(40 + bits + D)
+    K = torch.randn((NP, P, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(torch.float16)
+    V = torch.randn((NP, P, Hkv, D), generator=gen, device=dev, dtype=torch.float32).to(torch.float16)
+    bt = np.random.default_rng(41).permutation(NP).astype(np.int32).reshape(B, mb)
+    lengths = np.full(B, mb * P, np.int32)
+    lengths[-1] -= 77
+    cfg = pq.PagedQuantizedKVConfig(bits=bits, page_size=P, group_size=g)
+    cache = pq.quantize_kv_pages(K, V, to_dev(bt, dev), to_dev(lengths, dev), cfg)
+    del K, V
+    q = torch.randn((B, 1, Hq, D), generator=gen, device=dev, dtype=torch.float32).to(torch.float16)
+    got = pq.paged_quantized_kv_gqa_decode_attention(q, cache, backend=f"metal_q{bits}")[:, 0].float().cpu().numpy()
+    kq, vq = cache.k_pages_q.cpu().numpy(), cache.v_pages_q.cpu().numpy()
+    ks, vs = cache.k_scales.cpu().numpy(), cache.v_scales.cpu().numpy()
+    qn = q[:, 0].float().cpu().numpy()
+    ident = np.arange(mb, dtype=np.int32)[None]
+    for b in range(B):
+        pages = bt[b]
+        ref = op.quantized_paged_attention(qn[b:b + 1], kq[pages], vq[pages], ks[pages], vs[pages], ident,
+                                           lengths[b:b + 1], g, bits)
+        assert_close(got[b:b + 1], ref, what=f"config 4 q{bits} D{D} sequence {b}")
+
+
+@pytest.mark.parametrize("bits", [8, 4])
 @pytest.mark.parametrize("D,g", [(128, 64), (64, 64), (16, 8)])
 def test_quantize_pages_matches_oracle(dev, bits, D, g):
     rng = np.random.default_rng(90)

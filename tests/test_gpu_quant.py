@@ -155,7 +155,8 @@ def test_dot_rows_matvec_and_gate_up(dev, bits, M, N, K, g, zk):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("M,N,K,g", [(4, 14336, 4096, 64), (6, 200, 1280, 64), (24, 90, 512, 32), (32, 64, 4096, 64)])
+@pytest.mark.parametrize("M,N,K,g", [(4, 14336, 4096, 64), (8, 14336, 4096, 64), (32, 14336, 4096, 64),
+                                     (6, 200, 1280, 64), (24, 90, 512, 32), (32, 64, 4096, 64)])
 def test_batched_gate_up(dev, bits, M, N, K, g):
     rng = np.random.default_rng(400 + M + N)
     _, sg_stored, sg, zg = quant_weight(rng, N, K, g, bits, "sym")
@@ -192,6 +193,32 @@ def test_matvec_dtypes_and_zeros(dev, bits, act, zeros_kind, sdt, M, N, K, g):
     ref = (oq.q4_matvec if bits == 4 else oq.q8_matvec)(xf, stored, s, z, g, act=act)
     assert got.dtype == ACT[act] and tuple(got.shape) == (M, N)
     assert_close(got, ref, rtol=1e-2 if act == "f16" else 2e-2, what=f"q{bits} {act} {zeros_kind}")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [1, 3, 8, 24, 40])
+@pytest.mark.parametrize("amp", [1.0, 1e-4])
+def test_matvec_one_hot_rows_are_exact_dequant(dev, bits, M, amp):
+    """x row m = e_{k_m}: y[m, n] is the dequantized weight W[n, k_m] rounded
+    to fp16 once (the reference's dequant, ops/quant_ops.py:191-212), so every
+    kernel path (v_dot2 rows, MFMA, two-column tiles) must reproduce it bit
+    for bit -- including groups whose fp16 scale is below 2^-10 (amp 1e-4),
+    where a scale pre-divided by 16 would become subnormal."""
+    rng = np.random.default_rng(17 + M + bits)
+    N, K, g = 160, 512, 64
+    codes, stored, s, z = quant_weight(rng, N, K, g, bits, "affine", "normal")
+    s = (s * amp).astype(np.float16).astype(np.float32)
+    ks = rng.integers(0, K, size=M)
+    ks[: min(M, 4)] = [0, 1, K - 2, K - 1][: min(M, 4)]  # even and odd columns, both ends
+    x = np.zeros((M, K), np.float16)
+    x[np.arange(M), ks] = 1.0
+    fn = qo.q4_matvec_decode if bits == 4 else qo.q8_matvec_decode
+    y = fn(to_dev(x, dev), to_dev(stored, dev), to_dev(s, dev, torch.float16), to_dev(z, dev, torch.float16),
+           group_size=g).cpu().numpy()
+    W = oq.dequant(codes, s, z, g, np.float16)
+    # equal as numbers (a code at its zero point gives +0 from the sum where
+    # the reference's (q - z) * s gives -0 for a negative scale)
+    assert np.array_equal(y, W[:, ks].T)
 
 
 @pytest.mark.parametrize("bits", [4, 8])
@@ -341,6 +368,14 @@ def test_mlp_block(dev, bits, preset, B, S, D, I, g):
                              bits=bits, group_size=g, intermediates=True)
     ulp_down = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(rint["down"].astype(np.float64)), 2.0 ** -14))) - 10)
     assert_close(out.reshape(-1, D), ref, extra=4 * ulp_down, what="mlp out")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("B", [8, 32])
+def test_mlp_block_full_size_batched(dev, bits, B):
+    """Config 2 at M = 8 and config 5's batch 32 through the all-HIP MLP block
+    (norm kernel, batched gate/up + SwiGLU, down + residual) at 4096/14336."""
+    test_mlp_block(dev, bits, "fused_experimental", B, 1, 4096, 14336, 64)
 
 
 def test_mlp_decode_step(dev):

@@ -355,3 +355,55 @@ def test_round_bf16_matches_torch_cast():
     v = (np.random.default_rng(0).standard_normal(20000) * 300).astype(np.float32)
     v[:4] = [0.0, -0.0, 1e-40, 3.0e38]
     assert np.array_equal(oq.round_bf16(v), torch.from_numpy(v).to(torch.bfloat16).float().numpy())
+
+
+# ------------------------------------------------------------ contiguous caches
+
+def test_contiguous_attention_equals_identity_paged_and_scalar_loop():
+    # a contiguous cache is the paged layout under the identity table
+    # (ops/paged_kv_ops.py:99-105): the two statements must agree exactly
+    rng = np.random.default_rng(30)
+    B, S, Hq, Hkv, D, P = 3, 24, 4, 2, 16, 4
+    K = rng.standard_normal((B, S, Hkv, D)).astype(np.float16)
+    V = rng.standard_normal((B, S, Hkv, D)).astype(np.float16)
+    q = rng.standard_normal((B, Hq, D)).astype(np.float16)
+    lengths = np.array([1, 13, 40])  # the last one clips to MAX_S
+    got = op.contiguous_attention(q, K, V, lengths)
+    bt = op.identity_block_table(B, S, P)
+    paged = op.paged_attention(q, K.reshape(B * S // P, P, Hkv, D), V.reshape(B * S // P, P, Hkv, D), bt, lengths)
+    assert np.array_equal(got, paged)
+    for b in range(B):
+        for h in range(Hq):
+            n = min(lengths[b], S)
+            ref = _online_softmax_scalar(q[b, h], K[b, :, h // 2], V[b, :, h // 2], n, 1 / math.sqrt(D))
+            assert np.allclose(got[b, h], ref, rtol=1e-9, atol=1e-12)
+
+
+def test_contiguous_update_touches_one_row_per_sequence():
+    rng = np.random.default_rng(31)
+    K = rng.standard_normal((2, 8, 2, 4)).astype(np.float16)
+    kn = rng.standard_normal((2, 2, 4)).astype(np.float16)
+    K2, V2 = op.contiguous_update(K, K, kn, kn, [3, 7])
+    assert np.array_equal(K2[0, 3], kn[0]) and np.array_equal(K2[1, 7], kn[1])
+    mask = np.ones(K.shape[:2], bool)
+    mask[0, 3] = mask[1, 7] = False
+    assert np.array_equal(K2[mask], K[mask])
+    K3, _ = op.contiguous_update(K, K, kn, kn, 5)  # a scalar position broadcasts
+    assert np.array_equal(K3[:, 5], kn)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_quantize_contiguous_respects_lengths(bits):
+    rng = np.random.default_rng(32 + bits)
+    B, S, H, D, g = 2, 6, 2, 64, 32
+    K = rng.standard_normal((B, S, H, D)).astype(np.float16)
+    kq, vq, ks, vs = op.quantize_contiguous(K, K, g, bits, lengths=[4, 6])
+    full = op.quantize_contiguous(K, K, g, bits)
+    assert np.array_equal(kq[0, :4], full[0][0, :4]) and np.array_equal(kq[1], full[0][1])
+    assert not kq[0, 4:].any() and not ks[0, 4:].any()
+    # dequantized rows past the length are 0; valid rows within the bound
+    D_ = D
+    deq = op.dequantize(op.unpack_last(kq, D_) if bits == 4 else kq, ks, g, bits)
+    assert not deq[0, 4:].any()
+    assert np.all(np.abs(deq[0, :4].astype(np.float64) - K[0, :4]) <=
+                  np.repeat(np.abs(ks[0, :4].astype(np.float64)), g, axis=-1) * 0.51 + 1e-3)
