@@ -32,6 +32,9 @@ extern "C" {
 #define MK_OK 0
 #define MK_ERR_INVALID (-1)
 #define MK_ERR_UNSUPPORTED (-2)
+/* mk_paged_decode_attention_noalloc only: the call needs more scratch than
+ * the library's fixed no-allocation buffer holds. */
+#define MK_ERR_SCRATCH (-3)
 
 #define MK_DT_F16 0
 #define MK_DT_BF16 1
@@ -269,6 +272,22 @@ int mk_paged_decode_attention(const void* q, const void* K_pages, const void* V_
                               int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t page_size,
                               int64_t max_blocks, int64_t num_pages, float scale, int dtype,
                               void* workspace, size_t workspace_bytes, void* stream);
+
+/* mk_paged_decode_attention without a workspace argument.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The split partials live in a fixed 16 MiB device array inside
+ * the library (one per device, held until the process ends); a shape whose
+ * partials exceed it returns MK_ERR_SCRATCH before anything is launched
+ * (config 3 needs 4.5 MiB).  The call allocates nothing.  Calls on one device
+ * share that array, so calls that overlap in time on one device (different
+ * streams, or host threads) race; serialise them on one stream.  The current
+ * device must be the device of q and of the stream. */
+int mk_paged_decode_attention_noalloc(const void* q, const void* K_pages, const void* V_pages,
+                                      const int32_t* block_table, const int32_t* lengths,
+                                      void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                      int64_t page_size, int64_t max_blocks, int64_t num_pages,
+                                      float scale, int dtype, void* stream);
 
 /* paged_quantized_kv_gqa_decode_attention -- ops/paged_quantized_kv_ops.py:632-661
  * (kernels/q8_paged_gqa_decode_attention.metal, q4_...).  Codes/scales as in

@@ -26,6 +26,8 @@
 // over several pairs gets (m, l, O) partials that a second kernel merges
 // (LSE merge, ops/attention_ops.py:534-550); one inside a single pair is
 // finished in place.
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -54,6 +56,9 @@ constexpr int kQSlots = MK_ATTN_QSLOTS;
 // Segments one pair may touch (one per block at most; the plan keeps a pair
 // within 64 blocks).
 constexpr int kMaxSegs = 64;
+// Size of the fixed scratch of mk_paged_decode_attention_noalloc (16 MiB:
+// split partials for about 1000 (pair or sequence) slots at Hq = 32, D = 128).
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
 
 // One segment of a pair: sequence, first and end position, page-list index
 // of its first page (bit 30: the segment is the whole sequence).
@@ -1393,6 +1398,37 @@ int fp16_args(PagedArgs& a, const void* q, const void* K_pages, const void* V_pa
   return MK_OK;
 }
 
+// ------------------------------------------------- no-allocation scratch
+// mk_paged_decode_attention_noalloc keeps its split partials in this
+// file-scope array instead of a caller workspace.  Each device that runs the
+// library holds its own copy for the life of the process.  In host code the
+// array's name is only a host-side handle: the device address of a device's
+// copy comes from hipGetSymbolAddress with that device current, cached per
+// device below, and only that address is ever passed to a kernel.
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch (looked up once per device).
+int noalloc_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return -(int)e - 1000;
+  if (dev < 0 || dev >= kMaxDevices) return MK_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return -(int)e - 1000;
+    if (!p || !mk_aligned(p, 256)) return MK_ERR_UNSUPPORTED;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MK_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1425,6 +1461,30 @@ int mk_paged_decode_attention(const void* q, const void* K_pages, const void* V_
   if (rc != MK_OK || B == 0) return rc;
   a.ws = reinterpret_cast<float*>(workspace);
   return attention_launch(a, D, 0, dtype, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mk_paged_decode_attention_noalloc(const void* q, const void* K_pages, const void* V_pages,
+                                      const int32_t* block_table, const int32_t* lengths,
+                                      void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                      int64_t page_size, int64_t max_blocks, int64_t num_pages,
+                                      float scale, int dtype, void* stream) {
+  PagedArgs a = {};
+  const int rc = fp16_args(a, q, K_pages, V_pages, block_table, lengths, out, B, Hq, Hkv, D,
+                           page_size, max_blocks, num_pages, scale, dtype);
+  if (rc != MK_OK || B == 0) return rc;
+  // The split plan is a pure function of the shape and the device's CU
+  // count; reject a call whose partials would not fit before touching the GPU.
+  if (fast_ok(D, 0, dtype, a.gs, a.P, a.NP, a.Hkv)) {
+    PagedArgs plan = a;
+    split_plan(plan, 0);
+    if (workspace_need(plan, D) > kNoAllocScratchBytes) return MK_ERR_SCRATCH;
+  }
+  void* ws = nullptr;
+  const int src = noalloc_scratch(&ws);
+  if (src != MK_OK) return src;
+  a.ws = reinterpret_cast<float*>(ws);
+  return attention_launch(a, D, 0, dtype, kNoAllocScratchBytes,
+                          reinterpret_cast<hipStream_t>(stream));
 }
 
 int mk_paged_quantized_decode_attention(const void* q, const uint8_t* K_q, const uint8_t* V_q,

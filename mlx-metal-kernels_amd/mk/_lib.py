@@ -29,6 +29,7 @@ LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 MK_OK = 0
 MK_ERR_INVALID = -1
 MK_ERR_UNSUPPORTED = -2
+MK_ERR_SCRATCH = -3
 
 DT_F16 = 0
 DT_BF16 = 1
@@ -71,6 +72,7 @@ SIGNATURES: dict[str, list] = {
     "mk_quantize_kv": [_P, _P, _P, _I64, _I64, _I64, _I, _I, _P],
     "mk_paged_attention_workspace_bytes": [_I64] * 6,
     "mk_paged_decode_attention": [_P] * 6 + [_I64] * 7 + [_F, _I, _P, _SZ, _P],
+    "mk_paged_decode_attention_noalloc": [_P] * 6 + [_I64] * 7 + [_F, _I, _P],
     "mk_paged_quantized_decode_attention": [_P] * 8 + [_I64] * 8 + [_I, _F, _I, _P, _SZ, _P],
 }
 _RESTYPES = {"mk_paged_attention_workspace_bytes": _SZ}
@@ -166,6 +168,9 @@ def launch(name: str, device: torch.device, *args) -> int:
             raise RuntimeError(f"{name}: invalid argument (status {rc})")
         if rc == MK_ERR_UNSUPPORTED:
             raise RuntimeError(f"{name}: unsupported shape/dtype combination (status {rc})")
+        if rc == MK_ERR_SCRATCH:
+            raise RuntimeError(f"{name}: the call needs more than the library's fixed 16 MiB "
+                               f"no-allocation scratch (status {rc}); use the workspace entry point")
         raise RuntimeError(f"{name}: HIP launch failed (hipError {-rc - 1000})")
     return rc
 
