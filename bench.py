@@ -39,6 +39,10 @@ HIDDEN, INTER, GROUP = 4096, 14336, 64
 DOMINANT_KERNEL = "gemv_dot_kernel<4, 2, 2, true, 1>"  # residual + RMSNorm + q4 gate/up + SwiGLU, M = 1
 COPY_KERNEL_HINT = "copy"                      # torch's device-to-device copy kernel
 TRAFFIC_SUMMARY = "gemv_dot_q4_rmsnorm_gate_up_M1_traffic.json"
+ATTN_TRAFFIC_SUMMARY = "paged_attn_config3_fp16_traffic.json"
+
+
+WORKLOADS = ("config3", "config4", "mlp_m4", "mlp_m8", "mlp_m32", "mlp_q8", "stack")
 
 
 def _parse():
@@ -50,13 +54,22 @@ def _parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the M=4/8, q8 and attention extras")
     ap.add_argument("--decode-stack-only", action="store_true",
-                    help="run only the config-5 decode stack extra and print its JSON (for profiling)")
+                    help="run only the config-5 decode stack extra and print its JSON (same as --workload stack)")
+    ap.add_argument("--workload", choices=WORKLOADS, default=None,
+                    help="run one workload alone and print its JSON (for profiling): config3 (paged fp16 "
+                         "attention), config4 (q8/q4 KV attention), mlp_m4 / mlp_m8 / mlp_m32 (batched q4 MLP "
+                         "steps), mlp_q8 (q8 MLP step, M=1), stack (config-5 decode stack)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="first run a plain device copy of this many MiB (counter calibration)")
     ap.add_argument("--summarize-counters", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE run, "
                          "WRITE_SIZE run, both with --calib-copy-mb) into the traffic summary and exit")
     ap.add_argument("--summary-out", default=os.path.join(ROOT, "profiles", TRAFFIC_SUMMARY))
+    ap.add_argument("--summary-kernel", default=DOMINANT_KERNEL,
+                    help="kernel-name substring the traffic summary is for (default: the MLP front kernel)")
+    ap.add_argument("--summary-workload", default="config2 residual+RMSNorm+gate/up 2x14336x4096 q4 g64 M=1")
+    ap.add_argument("--summary-bytes", type=int, default=0,
+                    help="algorithmic bytes per launch of that kernel (default: the MLP front's)")
     return ap.parse_args()
 
 
@@ -213,15 +226,22 @@ def attention_config3(dev, steps, warmup):
     nbytes = tot * Hkv * D * 2 * 2 + sum(math.ceil(int(n) / P) for n in lengths) * 4 + B * Hq * D * 2 * 2 + B * 4
     del caches, fns
     torch.cuda.empty_cache()
+    achieved = nbytes / (ms * 1e-3) / 1e9
     return {
         "workload": "config3_paged_gqa_fp16_B16_ctx_U512_8192",
         "tokens_per_s": B / (ms * 1e-3),
         "us_per_call": ms * 1e3,
         "kv_tokens": tot,
         "ns_per_kv_token": ms * 1e6 / tot,
-        "hbm_gbs": nbytes / (ms * 1e-3) / 1e9,
-        "frac_of_peak": nbytes / (ms * 1e-3) / 1e9 / PEAK_GBS,
+        "hbm_gbs": achieved,
+        "frac_of_peak": achieved / PEAK_GBS,
         "bytes": nbytes,
+        # the call is the split-context kernel plus the partial merge; both
+        # run on the stream the graph is launched on and are timed together
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": load_traffic(ATTN_TRAFFIC_SUMMARY),
+                     "kernel": "paged_attn_kernel<f16,128,0,false,true> + paged_attn_merge_kernel<f16,128>",
+                     "bytes_per_launch": nbytes, "us_per_launch": round(ms * 1e3, 3)},
     }
 
 
@@ -359,6 +379,12 @@ def cpu_baseline(sets, x_res_nw, budget_s=20.0):
 # ----------------------------------------------------------------- counters
 
 
+def _demangled(name):
+    """Kernel names as rocprofv3 writes them, without the anonymous-namespace
+    prefix (mangled names are matched as they are)."""
+    return name.replace("(anonymous namespace)::", "")
+
+
 def _counter_rows(path, counter):
     import csv
 
@@ -370,16 +396,16 @@ def _counter_rows(path, counter):
     return rows
 
 
-def summarize_counters(fetch_csv, write_csv, out_path, copy_mb):
-    """HBM traffic per launch of the dominant kernel from FETCH_SIZE and
-    WRITE_SIZE (KiB per dispatch), each scaled by what the same counter reads
-    for the plain copy of ``copy_mb`` MiB run by --calib-copy-mb."""
+def summarize_counters(fetch_csv, write_csv, out_path, copy_mb, kernel=DOMINANT_KERNEL, workload=None,
+                       algo_bytes=0):
+    """HBM traffic per launch of ``kernel`` from FETCH_SIZE and WRITE_SIZE
+    (KiB per dispatch), each scaled by what the same counter reads for the
+    plain copy of ``copy_mb`` MiB run by --calib-copy-mb."""
     copy_bytes = copy_mb * (1 << 20)
-    out = {"kernel": DOMINANT_KERNEL, "workload": "config2 residual+RMSNorm+gate/up 2x14336x4096 q4 g64 M=1",
-           "algorithmic_bytes": None, "copy_bytes": copy_bytes}
+    out = {"kernel": kernel, "workload": workload, "algorithmic_bytes": None, "copy_bytes": copy_bytes}
     for name, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
         rows = _counter_rows(path, name)
-        dom = [v for k, v in rows if DOMINANT_KERNEL in k.replace("(anonymous namespace)::", "")]
+        dom = [v for k, v in rows if kernel in _demangled(k)]
         cop = [v for k, v in rows if COPY_KERNEL_HINT in k.lower() and "gemv" not in k]
         if not dom or not cop:
             raise SystemExit(f"{name}: kernel rows not found in {path}")
@@ -391,18 +417,18 @@ def summarize_counters(fetch_csv, write_csv, out_path, copy_mb):
                      "copy_kib": round(max(cop), 1), "scale": round(factor, 4),
                      "bytes_per_launch": int(per_launch_kib * 1024.0 * factor)}
     out["traffic_bytes_per_launch"] = out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"]
-    b_front, _ = mlp_bytes(1, 4)
-    out["algorithmic_bytes"] = b_front
-    out["traffic_over_algorithmic"] = round(out["traffic_bytes_per_launch"] / b_front, 4)
+    algo = algo_bytes or mlp_bytes(1, 4)[0]
+    out["algorithmic_bytes"] = algo
+    out["traffic_over_algorithmic"] = round(out["traffic_bytes_per_launch"] / algo, 4)
     with open(out_path, "w") as f:
         json.dump(out, f, indent=2)
     print(json.dumps(out))
 
 
-def load_traffic():
-    """Measured HBM bytes per launch of the dominant kernel (profiles/), or None."""
+def load_traffic(name=TRAFFIC_SUMMARY):
+    """Measured HBM bytes per launch from a traffic summary in profiles/, or None."""
     try:
-        with open(os.path.join(ROOT, "profiles", TRAFFIC_SUMMARY)) as f:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
             return int(json.load(f)["traffic_bytes_per_launch"])
     except (OSError, ValueError, KeyError):
         return None
@@ -411,10 +437,40 @@ def load_traffic():
 # ----------------------------------------------------------------- main
 
 
+def mlp_extra(dev, sets, M, bits, steps, warmup=12):
+    """One batched / q8 MLP step (same kernels as the timed step) -> dict."""
+    import torch
+
+    s8 = [make_mlp_set(dev, 8, 200 + i) for i in range(4)] if bits == 8 else None
+    f8, _ = mlp_step_fns(s8 if bits == 8 else sets, M, bits, dev)
+    m_ms = time_steps([step for step, _ in f8], steps, warmup)
+    bb = sum(mlp_bytes(M, bits))
+    del f8, s8
+    torch.cuda.empty_cache()
+    return {"us_per_step": m_ms * 1e3, "hbm_gbs": bb / (m_ms * 1e-3) / 1e9,
+            "frac_of_peak": bb / (m_ms * 1e-3) / 1e9 / PEAK_GBS, "bytes": bb}
+
+
+def run_workload(name, dev, args):
+    """One workload alone (single-workload profiling runs)."""
+    if name == "config3":
+        return attention_config3(dev, max(50, args.steps // 3), 10)
+    if name == "config4":
+        return attention_config4(dev)
+    if name == "stack":
+        return decode_stack_config5(dev)
+    sets = [make_mlp_set(dev, 4, 100 + i) for i in range(args.sets)]
+    if name == "mlp_q8":
+        return {"workload": "q8_mlp_M1", **mlp_extra(dev, sets, 1, 8, max(60, args.steps // 3))}
+    M = int(name.split("_m")[1])
+    return {"workload": f"q4_mlp_M{M}", **mlp_extra(dev, sets, M, 4, max(60, args.steps // 3))}
+
+
 def main():
     args = _parse()
     if args.summarize_counters:
-        summarize_counters(*args.summarize_counters, args.summary_out, args.calib_copy_mb or 256)
+        summarize_counters(*args.summarize_counters, args.summary_out, args.calib_copy_mb or 256,
+                           kernel=args.summary_kernel, workload=args.summary_workload, algo_bytes=args.summary_bytes)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one GPU; multi-GPU runs are not part of it",
@@ -427,9 +483,6 @@ def main():
     dev = torch.device("cuda:0")
     _lib.load()
     torch.manual_seed(0)
-    if args.decode_stack_only:
-        print(json.dumps(decode_stack_config5(dev)), flush=True)
-        return
     if args.calib_copy_mb:
         src = torch.empty(args.calib_copy_mb << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
@@ -437,6 +490,11 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.decode_stack_only:
+        args.workload = "stack"
+    if args.workload:
+        print(json.dumps(run_workload(args.workload, dev, args)), flush=True)
+        return
 
     sets = [make_mlp_set(dev, 4, 100 + i) for i in range(args.sets)]
     set_bytes = sum(t.numel() * t.element_size() for ws in sets for m in ws for t in m)
@@ -453,20 +511,8 @@ def main():
 
     extra = {}
     if not args.no_extra:
-        for bits, M in ((4, 4), (4, 8), (8, 1)):
-            if bits == 8:
-                s8 = [make_mlp_set(dev, 8, 200 + i) for i in range(4)]
-                f8, _ = mlp_step_fns(s8, M, 8, dev)
-            else:
-                f8, _ = mlp_step_fns(sets, M, 4, dev)
-            m_ms = time_steps([step for step, _ in f8], max(60, args.steps // 3), 12)
-            bb = sum(mlp_bytes(M, bits))
-            extra[f"q{bits}_mlp_M{M}"] = {"us_per_step": m_ms * 1e3, "hbm_gbs": bb / (m_ms * 1e-3) / 1e9,
-                                          "frac_of_peak": bb / (m_ms * 1e-3) / 1e9 / PEAK_GBS}
-            del f8
-            if bits == 8:
-                del s8
-            torch.cuda.empty_cache()
+        for bits, M in ((4, 4), (4, 8), (4, 32), (8, 1)):
+            extra[f"q{bits}_mlp_M{M}"] = mlp_extra(dev, sets, M, bits, max(60, args.steps // 3))
         torch.cuda.empty_cache()
         extra["paged_attention"] = attention_config3(dev, max(50, args.steps // 3), 10)
         extra["quantized_attention"] = attention_config4(dev)

@@ -146,12 +146,14 @@ __device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
 }
 
 // Workgroup barrier for LDS data only.  __syncthreads() is also a global
-// memory fence, for which the compiler waits on every outstanding vector
-// load (vmcnt(0)); here only LDS writes must be complete (lgkmcnt(0)), so
-// weight loads issued earlier stay in flight across the barrier.
+// memory fence, for which the compiler waits on every outstanding vector load
+// (vmcnt(0)); here only the wave's LDS operations must be complete
+// (lgkmcnt(0)), so weight loads issued earlier stay in flight across the
+// barrier and are waited for where their registers are first used.  The
+// memory clobber keeps the compiler from moving LDS (or any memory) accesses
+// across it.
 __device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt=63 (no wait), expcnt=7, lgkmcnt=0
-  __builtin_amdgcn_s_barrier();
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // ---------------------------------------------------------------------------
