@@ -70,6 +70,12 @@ def _parse():
     ap.add_argument("--summary-workload", default="config2 residual+RMSNorm+gate/up 2x14336x4096 q4 g64 M=1")
     ap.add_argument("--summary-bytes", type=int, default=0,
                     help="algorithmic bytes per launch of that kernel (default: the MLP front's)")
+    ap.add_argument("--summarize-pmc", nargs=4, metavar=("CSV", "OUT_MD", "TITLE", "COMMAND"),
+                    help="turn one rocprofv3 --pmc counter_collection.csv (SQ counters) into a markdown "
+                         "summary for the kernels named by --summary-kernel (';'-separated substrings) and exit")
+    ap.add_argument("--summarize-stats", nargs=4, metavar=("CSV", "OUT_MD", "TITLE", "COMMAND"),
+                    help="turn one rocprofv3 --kernel-trace --stats kernel_stats.csv into a markdown table for the "
+                         "kernels named by --summary-kernel (';'-separated substrings) and exit")
     return ap.parse_args()
 
 
@@ -396,26 +402,54 @@ def _counter_rows(path, counter):
     return rows
 
 
+READ_REQ_COUNTERS = ("TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_128B_sum")
+
+
+def _dispatch_bytes(path, counter):
+    """(kernel name, bytes) per dispatch: from WRITE_SIZE / FETCH_SIZE (KiB),
+    or for reads from the L2->fabric request counts by size
+    (32 n32 + 64 n64 + 128 n128; the FETCH_SIZE expression reads 128-byte
+    requests through TCC_BUBBLE, which does not always count them)."""
+    import csv
+
+    per = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            d = per.setdefault(r["Dispatch_Id"], {"kernel": r.get("Kernel_Name", "")})
+            d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    out = []
+    for d in per.values():
+        if counter in d:
+            out.append((d["kernel"], d[counter] * 1024.0))
+        elif counter == "FETCH_SIZE" and "TCC_EA0_RDREQ_128B_sum" in d:
+            n32, n64, n128 = (d.get(c, 0.0) for c in READ_REQ_COUNTERS[1:])
+            out.append((d["kernel"], 32 * n32 + 64 * n64 + 128 * n128))
+    return out
+
+
 def summarize_counters(fetch_csv, write_csv, out_path, copy_mb, kernel=DOMINANT_KERNEL, workload=None,
                        algo_bytes=0):
-    """HBM traffic per launch of ``kernel`` from FETCH_SIZE and WRITE_SIZE
-    (KiB per dispatch), each scaled by what the same counter reads for the
-    plain copy of ``copy_mb`` MiB run by --calib-copy-mb."""
+    """HBM traffic per launch of ``kernel``: reads from one --pmc pass
+    (FETCH_SIZE, or the read-request counts by size), writes from a WRITE_SIZE
+    pass.  The plain copy of ``copy_mb`` MiB run by --calib-copy-mb reads and
+    writes exactly that many bytes; its reading is reported beside the
+    kernel's (``copy_ratio`` = counted / true) as the check of the counter."""
     copy_bytes = copy_mb * (1 << 20)
     out = {"kernel": kernel, "workload": workload, "algorithmic_bytes": None, "copy_bytes": copy_bytes}
     for name, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
-        rows = _counter_rows(path, name)
+        rows = _dispatch_bytes(path, name)
         dom = [v for k, v in rows if kernel in _demangled(k)]
+        # the calibration copy: copy-kernel dispatches whose count is nearest
+        # the copy's size
         cop = [v for k, v in rows if COPY_KERNEL_HINT in k.lower() and "gemv" not in k]
         if not dom or not cop:
             raise SystemExit(f"{name}: kernel rows not found in {path}")
-        # the calibration copy reads and writes copy_bytes once each; take its
-        # largest dispatch (the one of the known size)
-        factor = copy_bytes / (max(cop) * 1024.0)
-        per_launch_kib = sum(dom) / len(dom)
-        out[name] = {"kib_per_dispatch": round(per_launch_kib, 1), "dispatches": len(dom),
-                     "copy_kib": round(max(cop), 1), "scale": round(factor, 4),
-                     "bytes_per_launch": int(per_launch_kib * 1024.0 * factor)}
+        near = min(cop, key=lambda v: abs(math.log(max(v, 1.0) / copy_bytes)))
+        per_launch = sum(dom) / len(dom)
+        by_size = name == "FETCH_SIZE" and not _has_counter(path, "FETCH_SIZE")
+        out[name] = {"source": "TCC_EA0_RDREQ_{32B,64B,128B}_sum" if by_size else name,
+                     "dispatches": len(dom), "copy_ratio": round(near / copy_bytes, 4),
+                     "bytes_per_launch": int(per_launch)}
     out["traffic_bytes_per_launch"] = out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"]
     algo = algo_bytes or mlp_bytes(1, 4)[0]
     out["algorithmic_bytes"] = algo
@@ -423,6 +457,79 @@ def summarize_counters(fetch_csv, write_csv, out_path, copy_mb, kernel=DOMINANT_
     with open(out_path, "w") as f:
         json.dump(out, f, indent=2)
     print(json.dumps(out))
+
+
+def _has_counter(path, counter):
+    return bool(_counter_rows(path, counter))
+
+
+SIMDS = 256 * 4          # MI355X: 256 CUs x 4 SIMDs
+CLOCK_GHZ = 2.4          # MI355X peak engine clock
+VALU_CYCLES = 4          # a wave64 VALU instruction occupies a 16-lane SIMD for 4 cycles
+
+
+def summarize_pmc(csv_path, kernels, title, command, out_path=""):
+    """Markdown summary of SQ counters per dispatch (averaged over dispatches)
+    for each kernel-name substring in ``kernels``, with the busy fractions they
+    imply: MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x cycles), VALU busy =
+    SQ_INSTS_VALU x 4 / (SIMDs x cycles), cycles = dispatch duration x clock."""
+    import csv
+
+    per = {}
+    with open(csv_path, newline="") as f:
+        for r in csv.DictReader(f):
+            name = _demangled(r["Kernel_Name"])
+            key = next((k for k in kernels if k in name), None)
+            if key is None:
+                continue
+            d = per.setdefault(key, {}).setdefault(r["Dispatch_Id"], {"ns": 0})
+            d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+            d["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    lines = [f"# {title}", "", "Command (from the repository root on an MI355X box, ROCm 7.2):", "",
+             f"    {command}", "",
+             "then, to write this file:", "",
+             f"    python3 bench.py --summarize-pmc {csv_path} {out_path} '<title>' '<command>' "
+             f"--summary-kernel '{';'.join(kernels)}'", "",
+             f"Averages per dispatch; busy fractions over {SIMDS} SIMDs at {CLOCK_GHZ} GHz for the "
+             "dispatch's duration (VALU: 4 cycles per wave64 instruction).", ""]
+    for key in kernels:
+        disp = list(per.get(key, {}).values())
+        if not disp:
+            raise SystemExit(f"no dispatches of {key!r} in {csv_path}")
+        names = sorted({n for d in disp for n in d if n != "ns"})
+        avg = {n: sum(d.get(n, 0.0) for d in disp) / len(disp) for n in names}
+        ns = sorted(d["ns"] for d in disp)[len(disp) // 2]
+        cyc = SIMDS * ns * CLOCK_GHZ
+        lines += [f"## `{key}`", "", f"{len(disp)} dispatches, median duration {ns / 1e3:.2f} us", "",
+                  "| counter | per dispatch |", "|---|---:|"]
+        lines += [f"| {n} | {avg[n]:,.0f} |" for n in names]
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in avg:
+            lines.append(f"| MFMA busy (derived) | {avg['SQ_VALU_MFMA_BUSY_CYCLES'] / cyc:.3f} |")
+        if "SQ_INSTS_VALU" in avg:
+            lines.append(f"| VALU busy (derived) | {avg['SQ_INSTS_VALU'] * VALU_CYCLES / cyc:.3f} |")
+        if "SQ_WAVES" in avg and "SQ_INSTS_VALU" in avg:
+            lines.append(f"| VALU instructions per wave | {avg['SQ_INSTS_VALU'] / avg['SQ_WAVES']:,.0f} |")
+        lines.append("")
+    return "\n".join(lines)
+
+
+def summarize_stats(csv_path, kernels, title, command, out_path=""):
+    """Markdown table of a rocprofv3 --kernel-trace --stats kernel_stats.csv,
+    restricted to the kernels whose names contain one of ``kernels``."""
+    import csv
+
+    lines = [f"# {title}", "", "Command (from the repository root on an MI355X box, ROCm 7.2):", "",
+             f"    {command}", "", "then, to write this file:", "",
+             f"    python3 bench.py --summarize-stats {csv_path} {out_path} '<title>' '<command>' "
+             f"--summary-kernel '{';'.join(kernels)}'", "",
+             "| kernel | calls | avg us | min us | max us |", "|---|---:|---:|---:|---:|"]
+    with open(csv_path, newline="") as f:
+        for r in csv.DictReader(f):
+            name = _demangled(r["Name"])
+            if any(k in name for k in kernels):
+                lines.append(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                             f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} |")
+    return "\n".join(lines) + "\n"
 
 
 def load_traffic(name=TRAFFIC_SUMMARY):
@@ -468,6 +575,20 @@ def run_workload(name, dev, args):
 
 def main():
     args = _parse()
+    if args.summarize_stats:
+        csv_path, out_path, title, command = args.summarize_stats
+        text = summarize_stats(csv_path, args.summary_kernel.split(";"), title, command, out_path)
+        with open(out_path, "w") as f:
+            f.write(text)
+        print(text)
+        return
+    if args.summarize_pmc:
+        csv_path, out_path, title, command = args.summarize_pmc
+        text = summarize_pmc(csv_path, args.summary_kernel.split(";"), title, command, out_path)
+        with open(out_path, "w") as f:
+            f.write(text)
+        print(text)
+        return
     if args.summarize_counters:
         summarize_counters(*args.summarize_counters, args.summary_out, args.calib_copy_mb or 256,
                            kernel=args.summary_kernel, workload=args.summary_workload, algo_bytes=args.summary_bytes)

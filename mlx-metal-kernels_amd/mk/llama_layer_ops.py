@@ -16,7 +16,7 @@ composes.
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass
+from dataclasses import asdict, dataclass
 from typing import Any
 
 import torch
@@ -71,6 +71,15 @@ class LlamaLikeConfig:
 
     def qkv_output_dim(self) -> int:
         return self.q_output_dim() + 2 * self.kv_output_dim()
+
+    def to_dict(self) -> dict:
+        """models/llama_config.py:98-100 (the dataclass fields)."""
+        return asdict(self)
+
+    @classmethod
+    def from_dict(cls, data: dict) -> "LlamaLikeConfig":
+        """models/llama_config.py:102-104."""
+        return cls(**data).validate()
 
 
 def llama3_8b_like() -> LlamaLikeConfig:

@@ -84,6 +84,39 @@ def paged_attention(q, Kp, Vp, bt, lengths, scale=None):
     return attention(q, K, V, lengths, valid, scale)
 
 
+def verify_row_lengths(lengths, W: int) -> np.ndarray:
+    """[B, W] positions visible to each query row of a W-row verify pass:
+    draft token w sits at position lengths[b] - W + w and its staged decode
+    step attends over the positions up to and including its own
+    (ops/speculative_verify_ops.py:228-262: step i runs llama_stack_decode_step
+    at staged position `position + i` after the steps before it wrote their
+    K/V), so row w sees lengths[b] - (W - 1 - w) positions (none below 0)."""
+    lengths = np.asarray(lengths, dtype=np.int64)
+    return np.maximum(lengths[:, None] - (W - 1 - np.arange(W))[None, :], 0)
+
+
+def paged_verify_attention(q, Kp, Vp, bt, lengths, scale=None):
+    """The attention of the W staged decode steps of parallel_verify_tokens
+    (ops/speculative_verify_ops.py:161-296) in one call: q [B, W, Hq, D] ->
+    float64 [B, W, Hq, D], row w the single-token paged attention
+    (ops/gqa_ops.py:307-342) over verify_row_lengths(lengths, W)[:, w]
+    positions.  lengths[b] counts the context and all W new positions."""
+    W = q.shape[1]
+    rows = verify_row_lengths(lengths, W)
+    out = np.empty(q.shape, dtype=np.float64)
+    for w in range(W):
+        out[:, w] = paged_attention(q[:, w], Kp, Vp, bt, rows[:, w], scale)
+    return out
+
+
+def quantized_paged_verify_attention(q, kq, vq, ks, vs, bt, lengths, group_size, bits, scale=None):
+    """paged_verify_attention over q8/q4 pages (dequantized as
+    quantized_paged_attention does)."""
+    D = q.shape[-1]
+    K, V = dequantize_pages(kq, vq, ks, vs, group_size, bits, D)
+    return paged_verify_attention(q, K, V, bt, lengths, scale)
+
+
 # ----------------------------------------------------------------- RoPE
 
 

@@ -153,12 +153,16 @@ def test_full_shape_stack_step_with_llama3_head(dev, B):
     # the head on the HIP normalised row: the kernel tolerance
     assert_close(got_logits, oq.q4_matvec(final_hidden[:, 0].cpu().numpy(), *head, group_size=G),
                  what=f"head logits B={B}")
-    # end to end, relative to the logits' size
+    # end to end, relative to the logits' size: the layer output may differ
+    # from the oracle's by up to 4 fp16 ulps of the residual stream (checked
+    # above), i.e. a relative 4 * 2^-11 ~ 2e-3 per element, which the head's
+    # 4096-term dot product carries into each logit at the logits' rms scale
     rms = float(np.sqrt(np.mean(ref_logits.astype(np.float64) ** 2)))
-    assert_close(got_logits / rms, ref_logits / rms, what=f"end-to-end logits B={B}")
+    e2e_atol = 2 * 4 * 2.0 ** -11  # twice that bound, for the tail over 128256 logits
+    assert_close(got_logits / rms, ref_logits / rms, atol=e2e_atol, what=f"end-to-end logits B={B}")
     # the HIP argmax is np.argmax of the HIP logits exactly
     assert np.array_equal(got, np.argmax(got_logits, axis=-1))
     for b in range(B):
         if got[b] != want[b]:
             lg = ref_logits[b]
-            assert abs(lg[got[b]] - lg[want[b]]) <= 1e-2 * abs(lg[want[b]]) + 1e-3 * rms, (b, got[b], want[b])
+            assert abs(lg[got[b]] - lg[want[b]]) <= 1e-2 * abs(lg[want[b]]) + e2e_atol * rms, (b, got[b], want[b])

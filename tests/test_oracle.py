@@ -407,3 +407,93 @@ def test_quantize_contiguous_respects_lengths(bits):
     assert not deq[0, 4:].any()
     assert np.all(np.abs(deq[0, :4].astype(np.float64) - K[0, :4]) <=
                   np.repeat(np.abs(ks[0, :4].astype(np.float64)), g, axis=-1) * 0.51 + 1e-3)
+
+
+# ------------------------------------------------------- multi-row verify
+
+def _dense_causal_verify(q, K, V, lengths, scale):
+    """Brute force over a dense [W, S] score matrix with the causal mask
+    written out (j visible to row w iff j <= lengths[b] - W + w), scalar
+    softmax loops -- a different formulation from the oracle's per-row calls."""
+    B, W, Hq, D = q.shape
+    g = Hq // K.shape[2]
+    out = np.zeros(q.shape)
+    for b in range(B):
+        for w in range(W):
+            last = int(lengths[b]) - W + w  # the row's own position
+            for h in range(Hq):
+                scores = []
+                for j in range(K.shape[1]):
+                    if j <= last:
+                        scores.append((j, float(np.dot(q[b, w, h].astype(np.float64),
+                                                       K[b, j, h // g].astype(np.float64))) * scale))
+                if not scores:
+                    continue
+                mx = max(sc for _, sc in scores)
+                den = sum(math.exp(sc - mx) for _, sc in scores)
+                for j, sc in scores:
+                    out[b, w, h] += math.exp(sc - mx) / den * V[b, j, h // g].astype(np.float64)
+    return out
+
+
+def test_verify_attention_brute_force_and_row_lengths():
+    rng = np.random.default_rng(90)
+    B, W, Hq, Hkv, D, P, mb = 3, 4, 4, 2, 8, 4, 4
+    Kp = rng.standard_normal((B * mb, P, Hkv, D)).astype(np.float16)
+    Vp = rng.standard_normal((B * mb, P, Hkv, D)).astype(np.float16)
+    bt = rng.permutation(B * mb).astype(np.int32).reshape(B, mb)
+    q = rng.standard_normal((B, W, Hq, D)).astype(np.float16)
+    lengths = np.array([16, 7, 2])  # the last: rows 0 and 1 see nothing
+    assert op.verify_row_lengths(lengths, W).tolist() == [[13, 14, 15, 16], [4, 5, 6, 7], [0, 0, 1, 2]]
+    got = op.paged_verify_attention(q, Kp, Vp, bt, lengths)
+    K, _ = op.gather(Kp, bt, mb * P)
+    V, _ = op.gather(Vp, bt, mb * P)
+    ref = _dense_causal_verify(q, K, V, lengths, 1.0 / math.sqrt(D))
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
+    assert np.all(got[2, :2] == 0.0)
+    # W = 1 is the decode attention; the last row always is
+    assert np.array_equal(op.paged_verify_attention(q[:, -1:], Kp, Vp, bt, lengths)[:, 0],
+                          op.paged_attention(q[:, -1], Kp, Vp, bt, lengths))
+    assert np.array_equal(got[:, -1], op.paged_attention(q[:, -1], Kp, Vp, bt, lengths))
+
+
+def test_verify_attention_equals_staged_decode_loop_and_is_causal():
+    """The staged loop of parallel_verify_tokens (ops/speculative_verify_ops.py:
+    228-262) -- write draft token i's K/V at position p + i, then attend with
+    p + i + 1 positions -- against one multi-row call over the cache holding
+    all W writes; and a change at the last position reaches only the last row."""
+    rng = np.random.default_rng(91)
+    B, W, Hq, Hkv, D, P, mb = 2, 5, 8, 2, 16, 8, 4
+    Kp = rng.standard_normal((B * mb, P, Hkv, D)).astype(np.float16)
+    Vp = rng.standard_normal((B * mb, P, Hkv, D)).astype(np.float16)
+    bt = rng.permutation(B * mb).astype(np.int32).reshape(B, mb)
+    p = np.array([9, 20])
+    q = rng.standard_normal((B, W, Hq, D)).astype(np.float16)
+    kn = rng.standard_normal((B, W, Hkv, D)).astype(np.float16)
+    vn = rng.standard_normal((B, W, Hkv, D)).astype(np.float16)
+    K1, V1 = Kp, Vp
+    staged = []
+    for i in range(W):
+        K1, V1 = op.paged_kv_update(K1, V1, kn[:, i], vn[:, i], bt, p + i)
+        staged.append(op.paged_attention(q[:, i], K1, V1, bt, p + i + 1))
+    got = op.paged_verify_attention(q, K1, V1, bt, p + W)
+    assert np.array_equal(got, np.stack(staged, axis=1))
+    page, off = op.block_table_lookup(bt, p + W - 1, P)
+    K2 = K1.copy()
+    K2[page, off] += np.float16(1.0)
+    got2 = op.paged_verify_attention(q, K2, V1, bt, p + W)
+    assert np.array_equal(got2[:, :-1], got[:, :-1]) and not np.allclose(got2[:, -1], got[:, -1])
+
+
+def test_quantized_verify_attention_is_verify_over_dequantized_pages():
+    rng = np.random.default_rng(92)
+    B, W, Hq, Hkv, D, P, mb, g = 2, 3, 4, 1, 32, 4, 3, 16
+    Kp = rng.standard_normal((B * mb, P, Hkv, D)).astype(np.float16)
+    Vp = rng.standard_normal((B * mb, P, Hkv, D)).astype(np.float16)
+    bt = rng.permutation(B * mb).astype(np.int32).reshape(B, mb)
+    q = rng.standard_normal((B, W, Hq, D)).astype(np.float16)
+    for bits in (8, 4):
+        kq, vq, ks, vs = op.quantize_pages(Kp, Vp, g, bits)
+        Kd, Vd = op.dequantize_pages(kq, vq, ks, vs, g, bits, D)
+        got = op.quantized_paged_verify_attention(q, kq, vq, ks, vs, bt, [12, 5], g, bits)
+        assert np.array_equal(got, op.paged_verify_attention(q, Kd, Vd, bt, [12, 5]))
