@@ -1,0 +1,94 @@
+"""Host side of the speculative verify drop-in (ops/speculative_verify_ops.py):
+config and result rules, acceptance helpers (models/speculative_decoding.py:
+163-228, with the reference tests' cases), the torch reference verify
+attention against the oracle, and the row tables the HIP path uses.  No GPU."""
+
+import numpy as np
+import pytest
+import torch
+
+import mk.speculative_verify_ops as sv
+from oracle import paged as op
+from tests._data import assert_close
+
+
+def test_config_validation_and_dict():
+    cfg = sv.ParallelVerificationConfig().validate()
+    assert cfg.to_dict() == {"draft_length": 4, "mode": "greedy_exact", "backend_preset": "fused_experimental",
+                             "cache_layout": "contiguous", "use_prefill_for_draft": True, "return_logits": True,
+                             "commit_cache": False}
+    sv.ParallelVerificationConfig(cache_layout="paged").validate()
+    with pytest.raises(ValueError, match="draft_length must be positive"):
+        sv.ParallelVerificationConfig(draft_length=0).validate()
+    with pytest.raises(ValueError, match="mode must be 'greedy_exact'"):
+        sv.ParallelVerificationConfig(mode="sample").validate()
+    with pytest.raises(NotImplementedError, match="cache_layout"):
+        sv.ParallelVerificationConfig(cache_layout="ring").validate()
+
+
+def test_accept_mask_prefix_and_replacement():
+    # exact matching stops at the first mismatch; later matches do not count
+    assert sv.compute_accept_mask([1, 2, 3, 4], [1, 2, 9, 4]) == [True, True, False, False]
+    assert sv.compute_accept_mask([1, 2, 3, 4], [1, 2, 9, 4], require_exact_match=False) == [True, True, False, True]
+    assert sv.compute_accept_mask([5, 6], [5]) == [True, False]  # missing targets reject
+    assert sv.compute_accept_mask([], [1]) == []
+    assert sv.accepted_prefix_length([True, True, False, True]) == 2
+    vr = sv.verify_draft_tokens([1, 2, 3], [1, 7, 8])
+    assert (vr.accepted_count, vr.rejected_count, vr.replacement_token_id) == (1, 2, 7)
+    assert vr.all_committed_tokens() == [1, 7] and vr.rejected_tokens() == [2, 3]
+    full = sv.verify_draft_tokens([1, 2], [1, 2])
+    assert full.replacement_token_id is None and full.all_committed_tokens() == [1, 2]
+    res = sv.ParallelVerificationPassResult([1, 2, 3], [1, 7, 8], [True, False, False], 1, replacement_token_id=7)
+    assert res.accepted_tokens() == [1] and res.committed_tokens() == [1, 7]
+    assert res.to_verification_result().accepted_count == 1
+    empty = sv.parallel_verify_tokens(context_token_ids=[1], proposed_token_ids=[])
+    assert empty.accepted_count == 0 and empty.metadata["verification_path"] == "no_proposed_tokens"
+    with pytest.raises(ValueError, match="stack_cache is required"):
+        sv.parallel_verify_tokens(context_token_ids=[1], proposed_token_ids=[3])
+
+
+def test_target_tokens_first_maximum():
+    lg = [np.array([0.0, 3.0, 3.0, 1.0]), torch.tensor([[2.0, -1.0]])]
+    assert sv.target_tokens_from_verification_logits(lg, proposed_token_ids=[0, 0]) == [1, 0]
+    with pytest.raises(ValueError, match="greedy_exact"):
+        sv.target_tokens_from_verification_logits(lg, proposed_token_ids=[0, 0], mode="top_k")
+
+
+def test_embed_proposed_tokens():
+    emb = torch.arange(12, dtype=torch.float32).reshape(6, 2)
+    x = sv.embed_proposed_tokens([4, 0, 5], emb)
+    assert tuple(x.shape) == (1, 3, 2) and x[0, 0].tolist() == [8.0, 9.0]
+    with pytest.raises(NotImplementedError):
+        sv.embed_proposed_tokens([1], emb, B=2)
+    with pytest.raises(ValueError, match="non-empty"):
+        sv.embed_proposed_tokens([], emb)
+
+
+@pytest.mark.parametrize("W", [1, 3, 5])
+def test_reference_verify_attention_matches_oracle(W):
+    rng = np.random.default_rng(60 + W)
+    B, Hq, Hkv, D, P, mb = 3, 8, 2, 16, 4, 5
+    Kp = rng.standard_normal((B * mb, P, Hkv, D)).astype(np.float16)
+    Vp = rng.standard_normal((B * mb, P, Hkv, D)).astype(np.float16)
+    bt = rng.permutation(B * mb).astype(np.int32).reshape(B, mb)
+    q = rng.standard_normal((B, W, Hq, D)).astype(np.float16)
+    lengths = np.array([20, W + 1, max(1, W - 1)])
+    t = torch.from_numpy
+    got = sv.paged_verify_attention(t(q), t(Kp), t(Vp), t(bt), t(lengths), backend="reference")
+    assert_close(got, op.paged_verify_attention(q, Kp, Vp, bt, lengths), what=f"reference verify W={W}")
+
+
+def test_row_tables():
+    bt = torch.tensor([[3, 4], [7, 8]], dtype=torch.int32)
+    rows_bt, rows_len = sv._row_tables(bt, torch.tensor([10, 2], dtype=torch.int32), 3)
+    assert rows_bt.tolist() == [[3, 4]] * 3 + [[7, 8]] * 3
+    assert rows_len.tolist() == [8, 9, 10, 0, 1, 2]
+    assert np.array_equal(rows_len.numpy().reshape(2, 3), op.verify_row_lengths([10, 2], 3))
+
+
+def test_hip_verify_path_is_switched_off():
+    q = torch.zeros(1, 2, 8, 64, dtype=torch.float16)
+    K = torch.zeros(4, 16, 8, 64, dtype=torch.float16)
+    bt = torch.zeros(1, 4, dtype=torch.int32)
+    with pytest.raises((RuntimeError, ValueError)):
+        sv.paged_verify_attention(q, K, K, bt, 64)
