@@ -382,6 +382,65 @@ def cpu_baseline(sets, x_res_nw, budget_s=20.0):
     return med, len(times), blas
 
 
+def cpu_model():
+    """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def cpu_other_configs(budget_s=6.0):
+    """The oracle on this host for BASELINE configs 1 and 3, bounded samples:
+    config 1 = one q4 matvec 4096 x 4096, g64, M=1 (median of up to 10 runs);
+    config 3 = paged GQA decode attention (Hq 32 / Hkv 8, D=128, P=16) over
+    the first two of config 3's sequences (lengths U[512,8192], seed 3),
+    scaled to all 16 by KV tokens."""
+    import numpy as np
+
+    from oracle import paged as op
+    from oracle import quant as oq
+
+    out = {}
+    rng = np.random.default_rng(11)
+    codes = rng.integers(0, 16, size=(HIDDEN, HIDDEN // 2), dtype=np.uint8) | \
+        (rng.integers(0, 16, size=(HIDDEN, HIDDEN // 2), dtype=np.uint8) << 4)
+    sc = rng.uniform(0.002, 0.004, size=(HIDDEN, HIDDEN // GROUP)).astype(np.float16).astype(np.float32)
+    z = np.full(sc.shape, 8.0, np.float32)
+    x = rng.standard_normal((1, HIDDEN)).astype(np.float16)
+    oq.q4_matvec(x, codes, sc, z, GROUP)
+    times, t_end = [], time.perf_counter() + budget_s
+    while (time.perf_counter() < t_end or len(times) < 2) and len(times) < 10:
+        t0 = time.perf_counter()
+        oq.q4_matvec(x, codes, sc, z, GROUP)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    nbytes = HIDDEN * HIDDEN // 2 + 2 * HIDDEN * (HIDDEN // GROUP) * 2 + 2 * HIDDEN * 2
+    out["config1_q4_matvec_4096x4096_M1"] = {"ms_per_call": med * 1e3, "gbs": nbytes / med / 1e9,
+                                             "sample": f"{len(times)} calls, median"}
+    lengths = np.random.default_rng(3).integers(512, 8193, size=16)
+    Hq, Hkv, D, P = 32, 8, 128, 16
+    n = lengths[:2]
+    mb = int(np.ceil(n.max() / P))
+    Kp = rng.standard_normal((2 * mb, P, Hkv, D)).astype(np.float16)
+    Vp = rng.standard_normal((2 * mb, P, Hkv, D)).astype(np.float16)
+    bt = np.arange(2 * mb, dtype=np.int32).reshape(2, mb)
+    q = rng.standard_normal((2, Hq, D)).astype(np.float16)
+    t0 = time.perf_counter()
+    op.paged_attention(q, Kp, Vp, bt, n)
+    dt = (time.perf_counter() - t0) * float(lengths.sum()) / float(n.sum())
+    out["config3_paged_gqa_B16"] = {"ms_per_call": dt * 1e3, "tokens_per_s": 16 / dt,
+                                    "sample": f"sequences 0-1 ({int(n.sum())} of {int(lengths.sum())} KV positions), "
+                                              "scaled by KV positions"}
+    return out
+
+
 # ----------------------------------------------------------------- counters
 
 
@@ -649,6 +708,8 @@ def main():
             "kind": "port",
             "sample": f"{reps} q4 MLP decode steps (M=1, 4096/14336, g64) of the numpy oracle, median "
                       f"{med * 1e3:.1f} ms/step; BLAS threads {blas}, host cpu_count {os.cpu_count()}",
+            "cpu_model": cpu_model(),
+            "other_configs": cpu_other_configs(),
         }
 
     line = {
