@@ -698,6 +698,197 @@ __global__ __launch_bounds__(NMAT == 1 && BITS == 4 ? 1024 : 512) void gemv_tile
 }
 
 // --------------------------------------------------------------------------
+// Activation-stationary batched kernel (q4, fp16 activations and scales,
+// 5..32 rows, K % 256 == 0, K <= 4096): the MFMA kernels above re-read each
+// activation row from L2 for every 16-row weight tile, so at 32 rows the
+// activation reads (M x K x 2 bytes per tile) outweigh the 16 x K / 2 code
+// bytes they multiply.  Here a workgroup of K / 256 waves keeps the whole
+// activation block in registers -- wave w holds k in [256 w, 256 w + 256) of
+// every row, lane (r = l % 16, kb = l / 16) two 32-k runs, pre-permuted to
+// the order the weight unpack produces (64 VGPRs at 32 rows) -- and walks a
+// contiguous run of 16-row tiles: per tile each lane loads the 2 x 16 code
+// bytes of row r over its runs, the dequantized operand feeds the MT
+// column tiles' v_mfma_f32_16x16x32_f16 steps, and the K / 256 partial tiles
+// are summed through LDS (double buffered) by MT waves that take turns.  The
+// tile's scales and zero points (16 rows x G, contiguous) are staged in LDS
+// by the whole workgroup, one 16-byte vector per thread, instead of one
+// 2-byte gather per lane and group from every wave (which cost 30.5 against
+// 23.9 us with the gathers replaced by constants, gate/up at 8 rows).  One
+// barrier per tile publishes both the tile's partials and the next tile's
+// (s, z).  Measured, 2 x 14336 x 4096 gate/up + SwiGLU: 19.4 / 21.3 / 27.4 us
+// at 8 / 16 / 32 rows against 31.0 / 36.1 / 57.4 for the kernels above.
+// --------------------------------------------------------------------------
+template <int NMAT>
+struct XsBuf {
+  u32x4 w[NMAT][2];  // 32 code bytes: 64 k of row r
+  u32x4 sz;          // this thread's 16-byte vector of the tile's (s, z) block
+};
+
+// The runs: RUN = 128 puts them at 32 kb and 128 + 32 kb, so each load
+// instruction reads the 16 rows' aligned 64-byte half lines whole (used for
+// one column tile, where it measured 2 % faster); RUN = 32 makes them one
+// 64-k span at 64 kb, whose simpler addressing keeps the two-column-tile
+// kernel within 128 VGPRs.
+template <int NMAT, int MT, int EPI, int RUN>
+__global__ __launch_bounds__(1024) void gemv_xs_kernel(const GemvArgs args) {
+  constexpr int STEPS = 8;  // k32 MFMA steps per lane's 64 k (4 per run)
+  using Buf = XsBuf<NMAT>;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nw = args.kw;  // waves = K / 256
+  const int M = args.M, N = args.N, K = args.K, G = args.G;
+  const int r = lane & 15, kb = lane >> 4;
+  const int tiles = (N + 15) >> 4;
+  const int t_begin = blockIdx.x * args.rg;  // rg: tiles per workgroup
+  const int t_end = min(t_begin + args.rg, tiles);
+  const int ka = wave * 256 + kb * (RUN == 128 ? 32 : 64);  // run a: steps 0-3; run b = ka + RUN: 4-7
+  const uint32_t magic = in_vgpr(0x64006400u);
+  const uint32_t magic_hi = in_vgpr(0x54005400u);  // odd nibbles under 64.0h
+  const bool has_z = args.z[0] != nullptr;
+  const int ga = ka >> args.lg, gb = (ka + RUN) >> args.lg;  // g >= 32: one group per run
+
+  // LDS: [2][nw][NMAT * MT][64] f32x4 partial tiles, then [2][2 NMAT][16][G + 2]
+  // fp16 (s, z) slots (rows padded by 4 bytes: the 16 rows a read touches
+  // fall in 16 banks)
+  extern __shared__ __align__(16) uint8_t xs_lds[];
+  f32x4* red = reinterpret_cast<f32x4*>(xs_lds);
+  const int slab = nw * NMAT * MT * 64;  // f32x4 per partial buffer
+  const int gp = G + 2;
+  f16* szs = reinterpret_cast<f16*>(xs_lds + (size_t)2 * slab * sizeof(f32x4));
+  const int slot_len = 2 * NMAT * 16 * gp;
+
+  // this thread's (s, z) vector: piece p (s0, z0, s1, z1), row, 8 groups at c8
+  const int vec_per_piece = 2 * G;  // 16 rows x G / 8
+  const int nvec = 2 * NMAT * vec_per_piece;
+  const bool sz_live = tid < nvec;
+  const int vt = sz_live ? tid : 0;
+  const int sp = vt / vec_per_piece;
+  const int se = vt - sp * vec_per_piece;
+  const int srow = se / (G >> 3);
+  const int sc8 = se - srow * (G >> 3);
+  const bool s_zero = (sp & 1) && !has_z;  // zero points absent: z = 0
+  const f16* sbase = reinterpret_cast<const f16*>((sp & 1) && has_z ? args.z[sp >> 1] : args.s[sp >> 1]) +
+                     (size_t)srow * G + 8 * sc8;
+  const uint32_t code_off = (uint32_t)r * (uint32_t)args.row_bytes + (uint32_t)(ka >> 1);
+
+  // the activation block: column 16 mt + r (rows past M repeat row M - 1;
+  // their results are dropped)
+  u32x4 xp[MT][STEPS];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = min(16 * mt + r, M - 1);
+    const f16* xr = reinterpret_cast<const f16*>(args.x) + (size_t)m * K + ka;
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) xp[mt][st] = xperm<4, true>(ldg128(xr + (st >> 2) * RUN + 8 * (st & 3)));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // tile t's codes for row r and this thread's (s, z) vector (N % 16 == 0:
+  // every row of a tile exists); tiles past the run re-read its first
+  auto tile_of = [&](int t) { return __builtin_amdgcn_readfirstlane(t < t_end ? t : t_begin); };
+  auto issue_codes = [&](int t, int q, Buf& b) {
+    const uint8_t* p = args.w[q] + (size_t)tile_of(t) * 16 * args.row_bytes + code_off;
+    b.w[q][0] = ldg128_stream(p);
+    b.w[q][1] = ldg128_stream(p + RUN / 2);
+  };
+  auto issue_sz = [&](int t, u32x4& v) { v = ldg128(sbase + (size_t)tile_of(t) * 16 * G); };
+  auto issue = [&](int t, Buf& b) {
+#pragma unroll
+    for (int q = 0; q < NMAT; ++q) issue_codes(t, q, b);
+    issue_sz(t, b.sz);
+  };
+  auto stage_v = [&](const u32x4& v, int slot) {
+    if (sz_live) {
+      uint32_t* d = reinterpret_cast<uint32_t*>(szs + (size_t)(slot & 1) * slot_len + (sp * 16 + srow) * gp + 8 * sc8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) d[e] = s_zero ? 0u : v[e];
+    }
+  };
+  auto stage = [&](const Buf& b, int slot) { stage_v(b.sz, slot); };
+
+  // one tile: products against the staged (s, z), partials to LDS; the
+  // barrier and the reduction follow in the loop
+  auto compute_q = [&](const Buf& b, int it, int q) {
+    const f16* sl = szs + (size_t)(it & 1) * slot_len + r * gp;
+    f32x4* rb = red + (it & 1) * slab;
+    {
+      f32x4 acc[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int g = h ? gb : ga;
+        const GpMagic gpm = make_gp_magic(sl[(2 * q) * 16 * gp + g], sl[(2 * q + 1) * 16 * gp + g]);
+#pragma unroll
+        for (int st = 4 * h; st < 4 * h + 4; ++st) {
+          const u32x4 a = dq4_magic(b.w[q][h][st & 3], gpm, magic, magic_hi);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma_k32<f16>(a, xp[mt][st], acc[mt]);
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) rb[(wave * NMAT * MT + q * MT + mt) * 64 + lane] = acc[mt];
+    }
+  };
+  // the reducing waves sum the nw partials of tile t and store them (lane
+  // holds D[n = 4 kb + i][m = 16 mt + r])
+  auto reduce = [&](int t, int it) {
+    const f32x4* rb = red + (it & 1) * slab;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if (wave != (it * MT + mt) % nw) continue;
+      const int m = 16 * mt + r;
+      f32x4 v[NMAT];
+#pragma unroll
+      for (int q = 0; q < NMAT; ++q) {
+        v[q] = rb[(q * MT + mt) * 64 + lane];
+        for (int w = 1; w < nw; ++w) v[q] += rb[(w * NMAT * MT + q * MT + mt) * 64 + lane];
+      }
+      const int nb = t * 16 + 4 * kb;
+      if (m < M && t < t_end) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int nn = nb + i;
+          if (nn < N) store_out<f16, EPI>(args, (size_t)m * N + nn, v[0][i], v[NMAT - 1][i]);
+        }
+      }
+    }
+  };
+
+  // One code buffer: each matrix's codes are refilled with the next tile's as
+  // soon as its products are issued, and the (s, z) vector for tile t + 1 is
+  // issued at the start of tile t -- ahead of t + 1's codes, so staging it at
+  // the end of tile t waits for it alone and the barrier never waits for
+  // codes.  (Measured against a ring of two or three code buffers refilled
+  // after a whole tile, whose (s, z) wait also covered the next tile's codes:
+  // 19.4 against 24.0 us for the 2 x 14336 x 4096 gate/up at 8 rows.)  The
+  // loop refills the same registers in place every iteration, so no buffer
+  // is copied across it.  The steps for a tile past the run compute on
+  // re-read data and store nothing.
+  Buf b;
+  issue(t_begin, b);
+  __builtin_amdgcn_sched_barrier(0);
+  stage(b, 0);
+  __syncthreads();
+  int it = 0;
+  for (int t = t_begin; t < t_end; ++t, ++it) {
+    issue_sz(t + 1, b.sz);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < NMAT; ++q) {
+      compute_q(b, it, q);
+      __builtin_amdgcn_sched_barrier(0);
+      issue_codes(t + 1, q, b);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    stage(b, it + 1);
+    __syncthreads();
+    reduce(t, it);
+  }
+}
+
+// --------------------------------------------------------------------------
 // M <= 4 kernel: v_dot2_f32_f16 on (nearly) raw codes.
 //
 // A lane handles 32-k "units" (16 code bytes for q4, 32 for q8) of R output
@@ -850,12 +1041,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
   // fp16 values (gpw <= 64), fetched with 128-bit loads and stored at a fixed
   // stride of 64 entries so a row's run sits at a compile-time offset.  They
   // are requested first, then the activations, then the codes (vmcnt retires
-  // in issue order, so each later wait leaves the code loads in flight).
+  // in issue order, so each later wait leaves the code loads in flight).  With
+  // the norm prologue the activations go first: the prologue then waits for
+  // its L2-resident operands only, not for the (s, z) vectors from HBM
+  // (measured 15.3 -> 14.8 us at 2 x 14336 x 4096; the plain kernel keeps the
+  // (s, z) vectors first, 12.7 against 12.9 us).
   const int lsv = 8 - args.lg;      // log2(16-byte vectors per run), gpw = 8 << lsv
   const int nvec = NSEG << lsv;     // <= 64 * DOT_SZ_VEC (checked by the dispatcher)
   u32x4 szv[DOT_SZ_VEC];
   uint32_t sz_zero[DOT_SZ_VEC];
-  {
+  auto issue_sz = [&]() {
     // branch-free: lanes without a run (or a missing zero tensor) read a valid
     // vector of the same row and drop it, so every load counts in order for
     // vmcnt.  A partial last slice clamps its vectors to the row's last 8
@@ -878,8 +1073,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
       szv[j] = ldg128(base + (size_t)nr * G + min(g0 + 8 * e, G - 8));
       sz_zero[j] = (uint32_t)isz & (has_z ^ 1u);  // zero tensor absent: z = 0
     }
+  };
+  auto stage_sz = [&]() {
+#pragma unroll
+    for (int j = 0; j < DOT_SZ_VEC; ++j) {
+      const int v = lane + 64 * j;
+      if (v < nvec) {
+        const int seg = v >> lsv, e = v & ((1 << lsv) - 1);
+        *reinterpret_cast<u32x4*>(stage + seg * (2 * SEG_STRIDE) + e * 16) =
+            sz_zero[j] ? (u32x4){0u, 0u, 0u, 0u} : szv[j];
+      }
+    }
+  };
+  if constexpr (!NORM) {
+    issue_sz();
+    __builtin_amdgcn_sched_barrier(0);  // keep the small loads ahead of the rest
   }
-  __builtin_amdgcn_sched_barrier(0);  // keep the small loads ahead of the rest
 
   // activations: NORM -- 16-byte chunks c = threadIdx.x (+ blockDim.x) of x,
   // the residual and the norm weight, at most two per thread (the dispatcher
@@ -906,6 +1115,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     aw[0] = ldg128(wp + 8 * c0);
     aw[1] = ldg128(wp + 8 * c1c);
     if (!args.nres) ar[0] = ar[1] = (u32x4){0u, 0u, 0u, 0u};
+    __builtin_amdgcn_sched_barrier(0);
+    issue_sz();
   } else {
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
@@ -924,15 +1135,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
       if constexpr (BITS == 8) f.w[t][r][BITS == 4 ? 0 : 1] = ldg128_stream(p + 16);
     }
   __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int j = 0; j < DOT_SZ_VEC; ++j) {
-    const int v = lane + 64 * j;
-    if (v < nvec) {
-      const int seg = v >> lsv, e = v & ((1 << lsv) - 1);
-      *reinterpret_cast<u32x4*>(stage + seg * (2 * SEG_STRIDE) + e * 16) =
-          sz_zero[j] ? (u32x4){0u, 0u, 0u, 0u} : szv[j];
-    }
-  }
+  if constexpr (!NORM) stage_sz();
 
   if constexpr (NORM) {
     const int c0 = threadIdx.x, c1 = threadIdx.x + nthr;
@@ -982,6 +1185,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < 4; ++j) f.x[0][j] = *reinterpret_cast<const u32x4*>(xrow + k0 + 8 * j);
+    stage_sz();
   } else {
     __builtin_amdgcn_wave_barrier();
   }
@@ -1235,6 +1439,64 @@ int launch_tile(GemvArgs a, hipStream_t st) {
   return MK_OK;
 }
 
+// CUs of the current device, cached per device.
+inline int gemv_device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// the activation-stationary kernel takes 5..32-row batches of matrices with at
+// least this many 16-row tiles (fewer tiles than about two per CU leave the
+// per-workgroup activation load unamortised)
+constexpr int kXsMinRows = 5;
+constexpr int kXsMinTiles = 512;
+constexpr size_t kXsMaxLds = 160 * 1024;
+
+// partial tiles (double buffered) + two (s, z) slots with 4-byte row padding
+inline size_t xs_lds_bytes(int nw, int nmat, int mt, int G) {
+  return (size_t)2 * nw * nmat * mt * 64 * sizeof(f32x4) + (size_t)2 * 2 * nmat * 16 * (G + 2) * 2;
+}
+
+// Activation-stationary launch: K / 256 waves per workgroup, the 16-row tiles
+// dealt out in equal contiguous runs to at most one workgroup per CU (the
+// 128 KB partial buffer and 16 waves of <= 128 VGPRs fill a CU).
+template <int NMAT, int MT, int EPI>
+int launch_xs(GemvArgs a, hipStream_t st) {
+  const int tiles = (a.N + 15) / 16;
+  const int cus = gemv_device_cus();
+  const int tpw = (tiles + cus - 1) / cus;
+  a.rg = tpw;
+  a.kw = a.K / 256;
+  const dim3 grid((unsigned)((tiles + tpw - 1) / tpw));
+  const dim3 block((unsigned)(64 * a.kw));
+  const size_t lds = xs_lds_bytes(a.kw, NMAT, MT, a.G);
+  gemv_xs_kernel<NMAT, MT, EPI, MT == 1 ? 128 : 32><<<grid, block, lds, st>>>(a);
+  MK_CHECK_LAUNCH();
+  return MK_OK;
+}
+
+// q4 only, fp16 activations and scales, 256 <= K <= 4096 with K % 256 == 0,
+// power-of-two group >= 32 (one group per lane's 32-k run), 16-byte
+// aligned x and codes, and enough rows that every CU gets tiles to stream
+template <int BITS, int NMAT, int EPI>
+bool xs_eligible(const GemvArgs& a, int mt, int act_dt, int sc_dt) {
+  bool ok = BITS == 4 && EPI != EPI_ROPE_KV && act_dt == MK_DT_F16 && sc_dt == MK_DT_F16 && a.lg >= 5 &&
+            (a.K % 256) == 0 && a.K >= 256 && a.K <= 4096 &&
+            (a.N % 16) == 0 && a.N / 16 >= kXsMinTiles && mk_aligned(a.x, 16) && (size_t)a.row_bytes % 16 == 0 &&
+            (a.G % 8) == 0 && 4 * NMAT * a.G <= 64 * (a.K / 256) &&  // one (s, z) vector per thread
+            xs_lds_bytes(a.K / 256, NMAT, mt, a.G) <= kXsMaxLds;
+  for (int t = 0; t < NMAT; ++t)
+    ok = ok && mk_aligned(a.w[t], 16) && mk_aligned(a.s[t], 16) && (a.z[0] == nullptr || mk_aligned(a.z[t], 16));
+  return ok;
+}
+
 // fp16 activations and scales, power-of-two group >= 32, K % 128 == 0, 16-byte
 // aligned x and codes
 template <int NMAT>
@@ -1372,8 +1634,22 @@ int gemv_dispatch(GemvArgs a, int64_t M, int64_t N, int64_t K, int64_t gs, int a
     // fp16 projections on the fast layouts only (the caller falls back)
     if (act_dt != MK_DT_F16 || sc_dt != MK_DT_F16 || !fast) return MK_ERR_UNSUPPORTED;
   }
-  // 17-32 rows at a time through the two-column-tile kernel, the rest below
   int64_t m_done = 0;
+  // up to 32 rows at a time through the activation-stationary kernel
+  if constexpr (EPI != EPI_ROPE_KV) {
+    if (M >= kXsMinRows && xs_eligible<BITS, NMAT, EPI>(a, 1, act_dt, sc_dt)) {
+      while (M - m_done >= kXsMinRows && rc == MK_OK) {
+        GemvArgs b = a;
+        int64_t mrows = (M - m_done) < 32 ? (M - m_done) : 32;
+        if (mrows > 16 && !xs_eligible<BITS, NMAT, EPI>(a, 2, act_dt, sc_dt)) mrows = 16;
+        b.M = (int)mrows;
+        rows_from(b, m_done);
+        rc = mrows > 16 ? launch_xs<NMAT, 2, EPI>(b, st) : launch_xs<NMAT, 1, EPI>(b, st);
+        m_done += mrows;
+      }
+    }
+  }
+  // 17-32 rows at a time through the two-column-tile kernel, the rest below
   if (tile_eligible<NMAT>(a, act_dt, sc_dt)) {
     while (M - m_done >= 17 && rc == MK_OK) {
       GemvArgs b = a;

@@ -100,6 +100,15 @@ TILE_CASES = [
     (20, 16, 256, 256, "affine"),
     (4, 3000, 14336, 64, "sym"),
     (64, 96, 1536, 64, "sym"),
+    # the activation-stationary kernel (q4, N % 16 == 0 with >= 512 row
+    # tiles, K % 256 == 0, K <= 4096): two groups per lane's 64 k with an odd
+    # tile count, one and two column tiles, no zero points, 32 + 1 rows, a
+    # one-wave workgroup; N = 8200 takes the other kernels
+    (5, 8208, 2048, 32, "affine"),
+    (5, 8200, 2048, 32, "affine"),
+    (17, 8192, 4096, 128, "none"),
+    (33, 8192, 1024, 64, "sym"),
+    (12, 16384, 256, 64, "sym"),
 ]
 
 
