@@ -889,6 +889,157 @@ __global__ __launch_bounds__(1024) void gemv_xs_kernel(const GemvArgs args) {
 }
 
 // --------------------------------------------------------------------------
+// K-split batched kernel (q4, fp16 activations and scales, 5..32 rows, one
+// matrix, K % 128 == 0 with 2048 <= K <= 16384, N % 16 == 0): for the
+// matrices the activation-stationary kernel does not take -- long rows (the
+// 14336-k down projection) or too few row tiles to share one activation block
+// (o-proj, qkv).  One 16-row tile per workgroup of 16 waves; wave w takes an
+// equal run of the row's 128-k halves (7 at K = 14336) and requests all of its
+// codes up front (one 16-byte load per half: lane (r, kb) reads k in
+// [128 h + 32 kb, +32) of row r, so each instruction reads the 16 rows'
+// aligned 64-byte half lines), then walks its halves with the activations of
+// the next two in flight -- four v_mfma_f32_16x16x32_f16 steps per half and
+// column tile.  The tile's scales and zero points are staged in LDS once; the
+// 16 partial tiles meet in LDS at the end.  The earlier MFMA kernel loaded a
+// chunk's activations behind the next chunk's codes (so each chunk waited for
+// the whole prefetch) and gathered (s, z) per lane.
+// --------------------------------------------------------------------------
+constexpr int XK_WAVES = 16;
+constexpr int XK_MAX_HALVES = 8;  // 128-k halves per wave: K <= 16 x 8 x 128
+
+inline size_t xk_lds_bytes(int mt, int G) {
+  return (size_t)XK_WAVES * mt * 64 * sizeof(f32x4) + (size_t)2 * 16 * (G + 2) * 2;
+}
+
+template <int MT, int EPI>
+__global__ __launch_bounds__(1024) void gemv_xk_kernel(const GemvArgs args) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int M = args.M, N = args.N, K = args.K, G = args.G;
+  const int r = lane & 15, kb = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int H = K >> 7;
+  const int h0 = (H * wave) / XK_WAVES;
+  const int nh = (H * (wave + 1)) / XK_WAVES - h0;  // 1..XK_MAX_HALVES (checked by the dispatcher)
+  const uint32_t magic = in_vgpr(0x64006400u);
+  const uint32_t magic_hi = in_vgpr(0x54005400u);  // odd nibbles under 64.0h
+  const bool has_z = args.z[0] != nullptr;
+
+  // LDS: [16][MT][64] f32x4 partial tiles, then [2][16][G + 2] fp16 (s, z)
+  extern __shared__ __align__(16) uint8_t xk_lds[];
+  f32x4* red = reinterpret_cast<f32x4*>(xk_lds);
+  const int gp = G + 2;
+  f16* szs = reinterpret_cast<f16*>(xk_lds + (size_t)XK_WAVES * MT * 64 * sizeof(f32x4));
+  __shared__ int rk_slots[EPI == EPI_ROPE_KV ? kRopeRows : 1];
+
+  // (s, z) of the tile: 16-byte vectors v = tid and tid + 1024 (piece, row,
+  // 8 groups), requested first so staging them waits for nothing else
+  const int vpp = 2 * G;  // vectors per piece: 16 rows x G / 8
+  u32x4 szv[2];
+  int szo[2];
+  bool szl[2], szz[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int v = tid + 1024 * j;
+    szl[j] = v < 2 * vpp;
+    const int vv = szl[j] ? v : 0;
+    const int p = vv / vpp, e = vv - p * vpp;
+    const int row = e / (G >> 3), c8 = e - row * (G >> 3);
+    szz[j] = p == 1 && !has_z;
+    const f16* base = reinterpret_cast<const f16*>(p == 1 && has_z ? args.z[0] : args.s[0]);
+    szv[j] = ldg128(base + (size_t)(n0 + row) * G + 8 * c8);
+    szo[j] = (p * 16 + row) * gp + 8 * c8;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // activations of half i in slot i % XR (the first XR requested before the
+  // codes, the rest as slots free up; a ring of four measured no faster):
+  // column 16 mt + r, k = 128 h + 32 kb + 8 s.  With one column tile the
+  // columns past M are zero and not loaded (half the activation traffic at
+  // 5..8 rows); results past M are dropped.
+  constexpr int XR = 2;
+  const f16* xr[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    xr[mt] = reinterpret_cast<const f16*>(args.x) + (size_t)min(16 * mt + r, M - 1) * K + 32 * kb;
+  u32x4 xs[XR][MT][4];
+  auto load_x = [&](int i, int slot) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if (MT == 2 || r < M) {  // two column tiles: rows past M repeat row M - 1 (no branch)
+#pragma unroll
+        for (int st = 0; st < 4; ++st) xs[slot][mt][st] = ldg128(xr[mt] + 128 * (h0 + i) + 8 * st);
+      } else {
+#pragma unroll
+        for (int st = 0; st < 4; ++st) xs[slot][mt][st] = (u32x4){0u, 0u, 0u, 0u};
+      }
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < XR; ++i)
+    if (i < nh) load_x(i, i);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // all of this wave's codes
+  const uint8_t* wr = args.w[0] + (size_t)(n0 + r) * args.row_bytes + 16 * kb;
+  u32x4 w[XK_MAX_HALVES];
+#pragma unroll
+  for (int i = 0; i < XK_MAX_HALVES; ++i)
+    if (i < nh) w[i] = ldg128_stream(wr + 64 * (h0 + i));
+  __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (szl[j]) {
+      uint32_t* d = reinterpret_cast<uint32_t*>(szs + szo[j]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) d[e] = szz[j] ? 0u : szv[j][e];
+    }
+  __syncthreads();
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const f16* sl = szs + r * gp;
+#pragma unroll
+  for (int i = 0; i < XK_MAX_HALVES; ++i) {
+    if (i < nh) {
+      const int g = (128 * (h0 + i) + 32 * kb) >> args.lg;
+      const GpMagic gpm = make_gp_magic(sl[g], sl[16 * gp + g]);
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const u32x4 a = dq4_magic(w[i][st], gpm, magic, magic_hi);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma_k32<f16>(a, xperm<4, true>(xs[i % XR][mt][st]), acc[mt]);
+      }
+      if (i + XR < nh) load_x(i + XR, i % XR);
+    }
+  }
+
+  // the 16 partial tiles; wave j finishes column tile j (lane holds
+  // D[n = 4 kb + i][m = 16 j + r])
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) red[(wave * MT + mt) * 64 + lane] = acc[mt];
+  if constexpr (EPI == EPI_ROPE_KV) rope_fill_slots(args, rk_slots);
+  __syncthreads();
+  if (wave >= MT) return;
+  const int mt = wave;
+  const int m = 16 * mt + r;
+  f32x4 v = red[mt * 64 + lane];
+  for (int ww = 1; ww < XK_WAVES; ++ww) v += red[(ww * MT + mt) * 64 + lane];
+  if (m >= M) return;
+  const int nb = n0 + 4 * kb;
+  if constexpr (EPI == EPI_ROPE_KV) {
+    rope_kv_pair(args, rk_slots, m, nb, v[0], v[1]);
+    rope_kv_pair(args, rk_slots, m, nb + 2, v[2], v[3]);
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) store_out<f16, EPI>(args, (size_t)m * N + nb + i, v[i], v[i]);
+}
+
+// --------------------------------------------------------------------------
 // M <= 4 kernel: v_dot2_f32_f16 on (nearly) raw codes.
 //
 // A lane handles 32-k "units" (16 code bytes for q4, 32 for q8) of R output
@@ -1459,6 +1610,30 @@ constexpr int kXsMinRows = 5;
 constexpr int kXsMinTiles = 512;
 constexpr size_t kXsMaxLds = 160 * 1024;
 
+// K-split launch: one 16-row tile per workgroup of 16 waves
+template <int MT, int EPI>
+int launch_xk(GemvArgs a, hipStream_t st) {
+  const dim3 grid((unsigned)(a.N / 16));
+  const dim3 block(64 * XK_WAVES);
+  gemv_xk_kernel<MT, EPI><<<grid, block, xk_lds_bytes(MT, a.G), st>>>(a);
+  MK_CHECK_LAUNCH();
+  return MK_OK;
+}
+
+// q4, one matrix, fp16 activations and scales, power-of-two group >= 32,
+// K % 128 == 0 with 16 <= K / 128 <= 16 x 8, N % 16 == 0, the tile's (s, z)
+// within two 16-byte vectors per thread, 16-byte aligned operands
+template <int BITS, int NMAT>
+bool xk_eligible(const GemvArgs& a, int mt, int act_dt, int sc_dt) {
+  const int H = a.K / 128;
+  bool ok = BITS == 4 && NMAT == 1 && act_dt == MK_DT_F16 && sc_dt == MK_DT_F16 && a.lg >= 5 &&
+            (a.K % 128) == 0 && H >= XK_WAVES && H <= XK_WAVES * XK_MAX_HALVES && (a.N % 16) == 0 &&
+            (a.G % 8) == 0 && 4 * a.G <= 2 * 64 * XK_WAVES && xk_lds_bytes(mt, a.G) <= kXsMaxLds &&
+            mk_aligned(a.x, 16) && (size_t)a.row_bytes % 16 == 0 && mk_aligned(a.w[0], 16) &&
+            mk_aligned(a.s[0], 16) && (a.z[0] == nullptr || mk_aligned(a.z[0], 16));
+  return ok;
+}
+
 // partial tiles (double buffered) + two (s, z) slots with 4-byte row padding
 inline size_t xs_lds_bytes(int nw, int nmat, int mt, int G) {
   return (size_t)2 * nw * nmat * mt * 64 * sizeof(f32x4) + (size_t)2 * 2 * nmat * 16 * (G + 2) * 2;
@@ -1645,6 +1820,20 @@ int gemv_dispatch(GemvArgs a, int64_t M, int64_t N, int64_t K, int64_t gs, int a
         b.M = (int)mrows;
         rows_from(b, m_done);
         rc = mrows > 16 ? launch_xs<NMAT, 2, EPI>(b, st) : launch_xs<NMAT, 1, EPI>(b, st);
+        m_done += mrows;
+      }
+    }
+  }
+  // otherwise up to 32 rows at a time through the K-split kernel
+  if constexpr (NMAT == 1) {
+    if (M - m_done >= kXsMinRows && xk_eligible<BITS, NMAT>(a, 1, act_dt, sc_dt)) {
+      while (M - m_done >= kXsMinRows && rc == MK_OK) {
+        GemvArgs b = a;
+        int64_t mrows = (M - m_done) < 32 ? (M - m_done) : 32;
+        if (mrows > 16 && !xk_eligible<BITS, NMAT>(a, 2, act_dt, sc_dt)) mrows = 16;
+        b.M = (int)mrows;
+        rows_from(b, m_done);
+        rc = mrows > 16 ? launch_xk<2, EPI>(b, st) : launch_xk<1, EPI>(b, st);
         m_done += mrows;
       }
     }

@@ -106,6 +106,13 @@ TILE_CASES = [
     # one-wave workgroup; N = 8200 takes the other kernels
     (5, 8208, 2048, 32, "affine"),
     (5, 8200, 2048, 32, "affine"),
+    # the K-split kernel (q4, one matrix, N % 16 == 0, K % 128 == 0 with
+    # 2048 <= K <= 16384): the down projection's 14336 k (7 halves per wave),
+    # one half per wave with two groups per half, two column tiles with
+    # uneven halves per wave and no zero points
+    (8, 4096, 14336, 64, "sym"),
+    (5, 1024, 2048, 32, "affine"),
+    (20, 2048, 6272, 128, "none"),
     (17, 8192, 4096, 128, "none"),
     (33, 8192, 1024, 64, "sym"),
     (12, 16384, 256, 64, "sym"),
