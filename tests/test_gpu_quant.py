@@ -282,7 +282,11 @@ def test_gate_up_and_swiglu_epilogue(dev, bits, rows, N, K, g):
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("rows,N,K,g,act", [(1, 14336, 4096, 64, "f16"), (1, 300, 3072, 64, "f16"),
                                             (1, 256, 4096, 32, "f16"), (3, 50, 96, 32, "f16"),
-                                            (1, 64, 512, 64, "bf16")])
+                                            (1, 64, 512, 64, "bf16"),
+                                            # 5..16 rows: norm kernel, then the activation-stationary
+                                            # gate/up (two groups per run at g = 32)
+                                            (8, 14336, 4096, 64, "f16"), (5, 8192, 2048, 32, "f16"),
+                                            (16, 8192, 1024, 128, "f16")])
 def test_rmsnorm_gate_up(dev, bits, rows, N, K, g, act):
     """mk_q{4,8}_rmsnorm_gate_up (one launch for a q4 fp16 row, the norm and
     gate/up kernels otherwise) against the separate norm kernel and the oracle."""
