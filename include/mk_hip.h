@@ -254,11 +254,15 @@ int mk_quantize_kv(const void* src, uint8_t* codes, f16_storage_t* scales, int64
 
 /* ---------------------------------------------------------------- paged decode attention */
 
-/* Scratch (bytes, 16-byte aligned, any content) the split-context attention
- * kernels need for B sequences of at most max_blocks pages, Hq query / Hkv
- * key-value heads of dimension D, on the current device.  Calls that may
- * run concurrently need distinct workspaces.  No reference counterpart: the
- * reference's one-thread-per-head kernels do not split the context. */
+/* Workspace (bytes, 16-byte aligned) the split-context attention kernels
+ * need for B sequences of at most max_blocks pages, Hq query / Hkv key-value
+ * heads of dimension D, on the current device.  Its first 64 KiB hold
+ * arrival counters: fill the workspace with zeros once, before its first
+ * call; every call leaves the counters zero again, so the buffer can then be
+ * reused without clearing (the rest holds split partials, any content).
+ * Calls that may run concurrently need distinct workspaces.  No reference
+ * counterpart: the reference's one-thread-per-head kernels do not split the
+ * context. */
 size_t mk_paged_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
                                           int64_t max_blocks, int64_t page_size);
 
@@ -276,8 +280,9 @@ int mk_paged_decode_attention(const void* q, const void* K_pages, const void* V_
 /* mk_paged_decode_attention without a workspace argument.  No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  The split partials live in a fixed 16 MiB device array inside
- * the library (one per device, held until the process ends); a shape whose
+ * hipMalloc).  The split partials and arrival counters live in a fixed
+ * 16 MiB device array inside the library (zero when the library loads, one
+ * per device, held until the process ends); a shape whose
  * partials exceed it returns MK_ERR_SCRATCH before anything is launched
  * (config 3 needs 4.5 MiB).  The call allocates nothing.  Calls on one device
  * share that array, so calls that overlap in time on one device (different

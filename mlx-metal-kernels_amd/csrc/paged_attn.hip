@@ -26,6 +26,11 @@
 // over several pairs gets (m, l, O) partials that a second kernel merges
 // (LSE merge, ops/attention_ops.py:534-550); one inside a single pair is
 // finished in place.
+// Short total contexts (few or short block-table rows, pages of a multiple
+// of 16 positions) take a one-kernel plan instead (paged_attn_sp_kernel):
+// splits laid out from the table width, merged in LDS within a workgroup and
+// across workgroups by the last one to arrive at a per-(sequence, kv head)
+// counter in the workspace.
 #include <mutex>
 
 #include "common.h"
@@ -93,6 +98,11 @@ struct PagedArgs {
   int min_split;       // fewest blocks per pair
   int units;           // (kv head, block of 16 query heads) waves per pair
   int wg_units;        // units per workgroup (a divisor of units, <= 8)
+  // short-context plan (paged_attn_sp_kernel): blocks per split, waves
+  // (splits) per workgroup, workgroups per (sequence, unit); sp_nw == 0
+  // selects the stream plan
+  int sp_blk, sp_nw, sp_nwg;
+  int* cnt;            // arrival counters [B][units], zero between calls
   float scale_log2;
 };
 
@@ -607,6 +617,28 @@ struct LaneOffsets {
   uint32_t vs[4];                  // V scale (elements)
 };
 
+// The lane offsets of the PT addressing mode for lane (r16, kb).
+template <int KVF, int D, bool SB>
+__device__ __forceinline__ LaneOffsets<KVF, D, SB> pt_lane_offsets(const PagedArgs& a, int r16, int kb) {
+  using F = Fmt<KVF, D>;
+  LaneOffsets<KVF, D, SB> lo;
+  const uint32_t rs = (uint32_t)a.Hkv * F::ROW_BYTES;  // bytes between positions of a page
+  lo.rs = rs;
+  lo.k0 = (uint32_t)r16 * rs + (uint32_t)(F::dbase(0, kb) * F::BITS / 8);
+  lo.v0 = (uint32_t)(4 * kb) * rs + (uint32_t)(r16 * F::VBYTES);
+  if constexpr (KVF != 0) {
+    const uint32_t ss = (uint32_t)a.Hkv * a.ngroups;  // scale elements between positions
+#pragma unroll
+    for (int e = 0; e < KVBlock<KVF, D, SB>::NKS; ++e) {
+      const int j = SB ? e * F::KRUN : e;
+      lo.ks[e] = (uint32_t)r16 * ss + (uint32_t)(F::dbase(j, kb) >> a.lg_gs);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lo.vs[i] = (uint32_t)(4 * kb + i) * ss + (uint32_t)((r16 * F::DPL) >> a.lg_gs);
+  }
+  return lo;
+}
+
 template <typename AT, int D, int KVF, bool SB, bool PT>
 __device__ __forceinline__ void load_block(KVBlock<KVF, D, SB>& blk, const PagedArgs& a,
                                            const SplitCtx& c, const LaneOffsets<KVF, D, SB>& lo,
@@ -859,6 +891,104 @@ __device__ __forceinline__ void write_segment(const PagedArgs& a, const f32x4* o
 // exact in fp16/bf16 exponent range); the O rescale runs only then.
 constexpr float kLazyMax = 8.0f;
 
+// One 32-position block of the online softmax: S = K q^T for its two
+// 16-position tiles, the (lazy) running max and sum, O += P V.  Lane
+// (r16, kb) holds m_run / l_run of head r16 and O[head 4kb + i][d slot j] in
+// o[j][i]; masked positions get p = 0 and a zeroed V row.
+template <typename AT, int D, int KVF, bool SB>
+__device__ __forceinline__ void consume_block(const KVBlock<KVF, D, SB> blk,
+                                              const u32x4 (&qv)[Fmt<KVF, D>::KSTEPS], float scale_log2,
+                                              int kb, float& m_run, float& l_run,
+                                              f32x4 (&o)[Fmt<KVF, D>::DPL]) {
+  constexpr int KSTEPS = Fmt<KVF, D>::KSTEPS;
+  constexpr int DPL = Fmt<KVF, D>::DPL;
+  // ---- S^T = K q^T for the two 16-position tiles
+  f32x4 sc[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) acc = mfma_k32<AT>(k_operand<AT, D, KVF, SB>(blk, u, j), qv[j], acc);
+    sc[u] = acc;
+  }
+  // ---- scores (base 2); lane holds S[16u + 4kb + i][head r16]
+  float sv[2][4];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sv[u][i] = sc[u][i] * scale_log2;
+  const bool full = blk.mask == 0xFFFFFFFFu;  // wave-uniform
+  if (!full) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (!((blk.mask >> (16 * u + 4 * kb + i)) & 1u)) sv[u][i] = -INFINITY;
+  }
+  float bmax = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
+                     fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
+  bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
+  bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+  // lazy max: raise m only when the block exceeds it by more than kLazyMax
+  const bool raise = bmax > m_run + kLazyMax;
+  const float m_new = raise ? bmax : m_run;
+  const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // an all-masked head keeps p = 0
+  float psum = 0.0f;
+  float p[2][4];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[u][i] = __builtin_amdgcn_exp2f(sv[u][i] - m_use);
+      psum += p[u][i];
+    }
+  }
+  psum += __shfl_xor(psum, 16, 64);
+  psum += __shfl_xor(psum, 32, 64);
+  if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform: some head's max moved
+    const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
+    l_run *= alpha;
+    // O lane holds O[head 4kb + i][column r16]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float al = __shfl(alpha, 4 * kb + i, 64);
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) o[j][i] *= al;
+    }
+  }
+  l_run += psum;
+  m_run = m_new;
+  const u32x4 pa = {pack_act2<AT>(p[0][0], p[0][1]), pack_act2<AT>(p[0][2], p[0][3]),
+                    pack_act2<AT>(p[1][0], p[1][1]), pack_act2<AT>(p[1][2], p[1][3])};
+
+  // ---- V operand chunks; masked positions are zeroed so stale or non-finite
+  // cache contents cannot reach the output through p = 0
+  u32x4 vc[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) vc[q] = v_chunk<D, KVF, SB>(blk, q);
+  if (!full) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int pos = q < 4 ? 4 * kb + q : 16 + 4 * kb + (q - 4);
+      if (!((blk.mask >> pos) & 1u)) vc[q] = (u32x4){0u, 0u, 0u, 0u};
+    }
+  }
+  // ---- O += P V, one MFMA per d slot
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) {
+    const int w = j >> 1;
+    u32x4 bop;
+    if (j & 1) {
+      bop = (u32x4){pack_hi16(vc[0][w], vc[1][w]), pack_hi16(vc[2][w], vc[3][w]),
+                    pack_hi16(vc[4][w], vc[5][w]), pack_hi16(vc[6][w], vc[7][w])};
+    } else {
+      bop = (u32x4){pack_lo16(vc[0][w], vc[1][w]), pack_lo16(vc[2][w], vc[3][w]),
+                    pack_lo16(vc[4][w], vc[5][w]), pack_lo16(vc[6][w], vc[7][w])};
+    }
+    o[j] = mfma_k32<AT>(pa, bop, o[j]);
+  }
+}
+
 template <typename AT, int D, int KVF, bool SB, bool PT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void paged_attn_kernel(
     const PagedArgs a) {
@@ -947,22 +1077,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
     for (int j = 0; j < KSTEPS; ++j) qslots[((s - 1) * KSTEPS + j) * 64 + lane] = qx[s - 1][j];
   LaneOffsets<KVF, D, SB> lo;
-  if constexpr (PT) {
-    const uint32_t rs = (uint32_t)a.Hkv * F::ROW_BYTES;  // bytes between positions of a page
-    lo.rs = rs;
-    lo.k0 = (uint32_t)r16 * rs + (uint32_t)(F::dbase(0, kb) * F::BITS / 8);
-    lo.v0 = (uint32_t)(4 * kb) * rs + (uint32_t)(r16 * F::VBYTES);
-    if constexpr (KVF != 0) {
-      const uint32_t ss = (uint32_t)a.Hkv * a.ngroups;  // scale elements between positions
-#pragma unroll
-      for (int e = 0; e < Blk::NKS; ++e) {
-        const int j = SB ? e * F::KRUN : e;
-        lo.ks[e] = (uint32_t)r16 * ss + (uint32_t)(F::dbase(j, kb) >> a.lg_gs);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) lo.vs[i] = (uint32_t)(4 * kb + i) * ss + (uint32_t)((r16 * DPL) >> a.lg_gs);
-    }
-  }
+  if constexpr (PT) lo = pt_lane_offsets<KVF, D, SB>(a, r16, kb);
 
   if constexpr (!PT) __syncthreads();
 
@@ -973,91 +1088,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   for (int j = 0; j < DPL; ++j) o[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   auto consume = [&](const Blk& blk) {
-    // ---- S^T = K q^T for the two 16-position tiles
-    f32x4 sc[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < KSTEPS; ++j) acc = mfma_k32<AT>(k_operand<AT, D, KVF, SB>(blk, u, j), qv[j], acc);
-      sc[u] = acc;
-    }
-    // ---- scores (base 2); lane holds S[16u + 4kb + i][head r16]
-    float sv[2][4];
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sv[u][i] = sc[u][i] * a.scale_log2;
-    const bool full = blk.mask == 0xFFFFFFFFu;  // wave-uniform
-    if (!full) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (!((blk.mask >> (16 * u + 4 * kb + i)) & 1u)) sv[u][i] = -INFINITY;
-    }
-    float bmax = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
-                       fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-    // lazy max: raise m only when the block exceeds it by more than kLazyMax
-    const bool raise = bmax > m_run + kLazyMax;
-    const float m_new = raise ? bmax : m_run;
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // an all-masked head keeps p = 0
-    float psum = 0.0f;
-    float p[2][4];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        p[u][i] = __builtin_amdgcn_exp2f(sv[u][i] - m_use);
-        psum += p[u][i];
-      }
-    }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform: some head's max moved
-      const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
-      l_run *= alpha;
-      // O lane holds O[head 4kb + i][column r16]
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float al = __shfl(alpha, 4 * kb + i, 64);
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) o[j][i] *= al;
-      }
-    }
-    l_run += psum;
-    m_run = m_new;
-    const u32x4 pa = {pack_act2<AT>(p[0][0], p[0][1]), pack_act2<AT>(p[0][2], p[0][3]),
-                      pack_act2<AT>(p[1][0], p[1][1]), pack_act2<AT>(p[1][2], p[1][3])};
-
-    // ---- V operand chunks; masked positions are zeroed so stale or non-finite
-    // cache contents cannot reach the output through p = 0
-    u32x4 vc[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) vc[q] = v_chunk<D, KVF, SB>(blk, q);
-    if (!full) {
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int pos = q < 4 ? 4 * kb + q : 16 + 4 * kb + (q - 4);
-        if (!((blk.mask >> pos) & 1u)) vc[q] = (u32x4){0u, 0u, 0u, 0u};
-      }
-    }
-    // ---- O += P V, one MFMA per d slot
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const int w = j >> 1;
-      u32x4 bop;
-      if (j & 1) {
-        bop = (u32x4){pack_hi16(vc[0][w], vc[1][w]), pack_hi16(vc[2][w], vc[3][w]),
-                      pack_hi16(vc[4][w], vc[5][w]), pack_hi16(vc[6][w], vc[7][w])};
-      } else {
-        bop = (u32x4){pack_lo16(vc[0][w], vc[1][w]), pack_lo16(vc[2][w], vc[3][w]),
-                      pack_lo16(vc[4][w], vc[5][w]), pack_lo16(vc[6][w], vc[7][w])};
-      }
-      o[j] = mfma_k32<AT>(pa, bop, o[j]);
-    }
+    consume_block<AT, D, KVF, SB>(blk, qv, a.scale_log2, kb, m_run, l_run, o);
   };
 
   // Blocks 2k and 2k+1 of the pair stream through buffers A and B.  Each
@@ -1139,6 +1170,268 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   }
   consume(Bq);  // the last odd block (or an empty one)
   write_segment<AT, D, KVF>(a, o, m_run, l_run, seg_at(sd, segC), pair, h0, hcount);
+}
+
+// ------------------------------------------------------- short-context plan
+// A small total context (B x blocks per block-table row x units at most
+// kSpMaxWaveBlocks) runs on a grid laid out from the block-table width
+// instead of the lengths.  Sequence b's 32-position blocks are cut into splits
+// of sp_blk blocks, one wave per (split, unit), and sp_nw consecutive splits
+// of one (sequence, unit) share a workgroup.  So nothing on the way to the
+// first K/V load waits for the lengths: the length, q and the split's page
+// ids are requested together.  The waves of a workgroup merge their (m, l, O)
+// in LDS.  A sequence covered by one workgroup is written final; otherwise
+// each workgroup stores one partial and counts itself in at the (sequence,
+// unit) arrival counter, and the workgroup that arrives last merges the
+// partials (LSE merge, ops/attention_ops.py:534-550), writes the output and
+// sets the counter back to zero -- the call is one kernel, and its counters
+// are zero again when it ends.  Workgroups past a sequence's last split exit
+// at once (the first of them writes zeros for an empty sequence).
+// Device-coherent (agent-scope) relaxed store of one float: it writes
+// through the per-XCD L2, so a partial written on one XCD reaches memory
+// without an L2 write-back.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Experiments: a fixed number of waves per workgroup (0: the plan's rule).
+#ifndef MK_ATTN_SP_NW
+#define MK_ATTN_SP_NW 0
+#endif
+#ifndef MK_ATTN_SP_MAXWB
+#define MK_ATTN_SP_MAXWB 16384
+#endif
+#ifndef MK_ATTN_SP_WAVES
+#define MK_ATTN_SP_WAVES 2048
+#endif
+constexpr int64_t kSpMaxWaveBlocks = MK_ATTN_SP_MAXWB;  // B x blocks x units on the short-context plan
+constexpr int64_t kSpWaves = MK_ATTN_SP_WAVES;          // waves it aims for (one round on 256 CUs)
+constexpr int kSpMergeTrip = 16;                        // partials the final merge reads per trip
+
+template <typename AT, int D, int KVF, bool SB>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void paged_attn_sp_kernel(
+    const PagedArgs a) {
+  using F = Fmt<KVF, D>;
+  using Blk = KVBlock<KVF, D, SB>;
+  constexpr int KSTEPS = F::KSTEPS;
+  constexpr int DPL = F::DPL;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nw = a.sp_nw;
+  const int r16 = lane & 15;
+  const int kb = lane >> 4;
+  // workgroup -> (its index within the sequence, sequence, unit); neighbouring
+  // workgroups take different units
+  const int unit = (int)blockIdx.x % a.units;
+  const int rest = (int)blockIdx.x / a.units;
+  const int b = rest % a.B;
+  const int wgi = rest / a.B;
+  const int hkv = unit / a.HB;
+  const int hb = unit - hkv * a.HB;
+  const int h0 = hkv * a.G + hb * 16;
+  const int hcount = min(16, a.G - hb * 16);
+  const int max_s = a.MB << a.lgP;
+  const int span = a.sp_blk * kBlockPos;     // positions per split
+  const int t0 = (wgi * nw + wave) * span;  // this wave's first position
+
+  // ---- requested together: the length, q and the split's page ids
+  const int len = clamp_len(a.lengths[b], max_s);
+  u32x4 qv[KSTEPS];
+  load_q<AT, D, KVF>(a, b, h0, hcount, r16, kb, qv);
+  const int pg0 = t0 >> a.lgP;
+  int my_page = -1;
+  {
+    const int npg = ((t0 + span - 1) >> a.lgP) - pg0 + 1;  // <= 64 (host: span <= 63 P)
+    if (lane < npg && pg0 + lane < a.MB) {
+      const int p = a.bt[(size_t)b * a.MB + pg0 + lane];
+      my_page = (p >= 0 && p < a.NP) ? p : -1;
+    }
+  }
+  const int nsplit = (nblk_of(len) + a.sp_blk - 1) / a.sp_blk;  // splits holding positions
+  const int nwg = (nsplit + nw - 1) / nw;                       // workgroups holding positions
+  if (wgi >= nwg) {  // workgroup-uniform
+    if (wgi == 0) {  // empty sequence
+      AT* op = reinterpret_cast<AT*>(a.out) + ((size_t)b * a.Hq + h0) * D;
+      for (int i = threadIdx.x; i < hcount * D; i += blockDim.x) op[i] = from_f32<AT>(0.0f);
+    }
+    return;
+  }
+  const int t1 = min(t0 + span, len);
+  const int nbt = t0 < t1 ? nblk_of(t1 - t0) : 0;  // wave-uniform
+
+  SplitCtx c;
+  c.spage = nullptr;
+  c.my_page = my_page;
+  c.blk0 = pg0;
+  c.po = 0;
+  c.t_begin = t0;
+  c.t_end = t1;
+  c.lgP = a.lgP;
+  c.Pm = (1 << a.lgP) - 1;
+  c.Hkv = a.Hkv;
+  c.hkv = hkv;
+  const LaneOffsets<KVF, D, SB> lo = pt_lane_offsets<KVF, D, SB>(a, r16, kb);
+
+  float m_run = -INFINITY;  // per head r16 (replicated over kb)
+  float l_run = 0.0f;
+  f32x4 o[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) o[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  auto consume = [&](const Blk& blk) {
+    consume_block<AT, D, KVF, SB>(blk, qv, a.scale_log2, kb, m_run, l_run, o);
+  };
+
+  // Blocks stream through buffers A and B, each refilled right after it is
+  // consumed; every load is issued on a path whose later waits are exact
+  // (no load sits under a branch that rejoins before its data is used).
+  if (nbt == 1) {  // wave-uniform
+    Blk A;
+    load_block<AT, D, KVF, SB, true>(A, a, c, lo, t0, r16, kb);
+    consume(A);
+  } else if (nbt > 1) {
+    // as in paged_attn_kernel: B starts empty, and a block index past the
+    // end reloads the last block, masked off
+    Blk A, Bq;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int r = 0; r < F::NRUN; ++r) Bq.k[u][r] = (u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int q = 0; q < 8; ++q) Bq.v[q] = (u32x4){0u, 0u, 0u, 0u};
+    if constexpr (KVF != 0) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < Blk::NKS; ++e) Bq.ks[u][e] = 0u;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) Bq.vs[q] = 0u;
+    }
+    Bq.mask = 0u;
+    for (int i = 0; i < nbt; i += 2) {
+      load_block<AT, D, KVF, SB, true>(A, a, c, lo, t0 + kBlockPos * i, r16, kb);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(Bq);
+      const bool has1 = i + 1 < nbt;
+      load_block<AT, D, KVF, SB, true>(Bq, a, c, lo, t0 + kBlockPos * (has1 ? i + 1 : i), r16, kb);
+      if (!has1) Bq.mask = 0u;
+      __builtin_amdgcn_sched_barrier(0);
+      consume(A);
+    }
+    consume(Bq);
+  }
+
+  // ---- the workgroup's splits, merged in LDS: wave w's O row of head h at
+  // so[(w * hcount + h) * D], its (m, l) at sm[(w * hcount + h) * 2]
+  extern __shared__ __align__(16) uint8_t attn_dyn[];
+  float* so = reinterpret_cast<float*>(attn_dyn);
+  float* sm = so + (size_t)nw * hcount * D;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int h = 4 * kb + i;
+    if (h >= hcount) continue;
+    float nat[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) nat[F::vslot(j)] = o[j][i];
+    float* dst = so + (size_t)(wave * hcount + h) * D + r16 * DPL;
+#pragma unroll
+    for (int e = 0; e < DPL / 4; ++e)
+      reinterpret_cast<f32x4*>(dst)[e] = (f32x4){nat[4 * e], nat[4 * e + 1], nat[4 * e + 2], nat[4 * e + 3]};
+  }
+  if (kb == 0 && r16 < hcount)
+    *reinterpret_cast<f32x2*>(sm + (size_t)(wave * hcount + r16) * 2) = (f32x2){m_run, l_run};
+  __syncthreads();
+
+  const bool single = nwg == 1;  // workgroup-uniform
+  // partial (g) of head h0 + h: row ((b * Hq + h0 + h) * sp_nwg + g)
+  const size_t prow = ((size_t)b * a.Hq + h0) * a.sp_nwg;
+  AT* out = reinterpret_cast<AT*>(a.out) + ((size_t)b * a.Hq + h0) * D;
+  for (int it = threadIdx.x; it < hcount * D; it += blockDim.x) {
+    const int h = it / D;
+    const int d = it - h * D;
+    float M = -INFINITY;
+    for (int w = 0; w < nw; ++w) M = fmaxf(M, sm[(w * hcount + h) * 2]);
+    const float Mu = M == -INFINITY ? 0.0f : M;
+    float L = 0.0f, O = 0.0f;
+    for (int w = 0; w < nw; ++w) {
+      const float e = __builtin_amdgcn_exp2f(sm[(w * hcount + h) * 2] - Mu);
+      L += sm[(w * hcount + h) * 2 + 1] * e;
+      O += so[(size_t)(w * hcount + h) * D + d] * e;
+    }
+    if (single) {
+      out[it] = from_f32<AT>(O * (L > 0.0f ? 1.0f / L : 0.0f));
+    } else {
+      const size_t row = prow + (size_t)h * a.sp_nwg + wgi;
+      store_agent(a.ws + row * D + d, O);
+      if (d == 0) {
+        store_agent(a.ws_ml + row * 2, M);
+        store_agent(a.ws_ml + row * 2 + 1, L);
+      }
+    }
+  }
+  if (single) return;
+
+  // ---- arrival.  The partials went out as device-coherent stores (they
+  // write through this XCD's L2); once every thread has seen them complete,
+  // one thread counts the workgroup in.  The last to arrive drops its
+  // cached lines (acquire: L1/L2 invalidate), reads the partials, merges them
+  // and clears the counter.  (A release fence would order the stores too,
+  // but its L2 write-back costs each workgroup more than the whole merge.)
+  __shared__ int is_last;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  lds_barrier();
+  if (threadIdx.x == 0) {
+    int* ctr = a.cnt + (size_t)b * a.units + unit;
+    const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev == nwg - 1;
+    if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = last;
+  }
+  lds_barrier();
+  if (!is_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  constexpr int DV = D / 4;  // 4-float chunks per head row
+  for (int it = threadIdx.x; it < hcount * DV; it += blockDim.x) {
+    const int h = it / DV;
+    const int dv = it - h * DV;
+    const size_t row0 = prow + (size_t)h * a.sp_nwg;
+    const f32x2* ml = reinterpret_cast<const f32x2*>(a.ws_ml) + row0;
+    const f32x4* po = reinterpret_cast<const f32x4*>(a.ws + row0 * D) + dv;  // partial g at po[g * DV]
+    // 16 partials per trip, all requested before any is used; the running
+    // (M, L, O) is rescaled when a trip raises the max
+    constexpr int CH = kSpMergeTrip;
+    float M = -INFINITY, L = 0.0f;
+    float O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int g0 = 0; g0 < nwg; g0 += CH) {
+      f32x2 v[CH];
+      f32x4 x[CH];
+#pragma unroll
+      for (int k = 0; k < CH; ++k) {
+        const int g = g0 + k < nwg ? g0 + k : nwg - 1;  // past the end: re-read, weight 0
+        v[k] = ml[g];
+        x[k] = po[(size_t)g * DV];
+      }
+      float Mc = M;
+#pragma unroll
+      for (int k = 0; k < CH; ++k) Mc = fmaxf(Mc, g0 + k < nwg ? v[k][0] : -INFINITY);
+      const float Mu = Mc == -INFINITY ? 0.0f : Mc;
+      const float r = __builtin_amdgcn_exp2f(M - Mu);  // 0 while M is -inf
+      L *= r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) O[e] *= r;
+#pragma unroll
+      for (int k = 0; k < CH; ++k) {
+        const float w = g0 + k < nwg ? __builtin_amdgcn_exp2f(v[k][0] - Mu) : 0.0f;
+        L += v[k][1] * w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) O[e] += x[k][e] * w;
+      }
+      M = Mc;
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    *reinterpret_cast<u32x2*>(out + h * D + 4 * dv) =
+        (u32x2){pack_act2<AT>(O[0] * inv, O[1] * inv), pack_act2<AT>(O[2] * inv, O[3] * inv)};
+  }
 }
 
 // --------------------------------------------------------------- generic path
@@ -1291,12 +1584,51 @@ inline void split_plan(PagedArgs& a, int kvf) {
   a.wg_units = pairs * (a.units / wg) >= cus ? wg : 1;
 }
 
-// Partial slots: pair + sequence < max_pairs + B.
+// Short-context plan (paged_attn_sp_kernel), taken when the block-table
+// width keeps B x blocks x units within kSpMaxWaveBlocks and pages hold a
+// multiple of 16 positions: blocks per split sized for about kSpWaves
+// waves, then the widest workgroup (8, 4 or 2 splits) that still gives every
+// CU a workgroup, no wider than the splits of a sequence, and with its LDS
+// merge buffer within 64 KiB.
+inline size_t sp_lds_bytes(const PagedArgs& a, int nw, int64_t D) {
+  return (size_t)nw * (a.G < 16 ? a.G : 16) * (D + 2) * sizeof(float);
+}
+inline void sp_plan(PagedArgs& a, int64_t D) {
+  a.sp_nw = 0;
+  if (a.P % 16 != 0) return;
+  const int64_t blk = ((int64_t)a.MB * a.P + kBlockPos - 1) / kBlockPos;
+  const int64_t wb = (int64_t)a.B * blk * a.units;
+  if (wb > kSpMaxWaveBlocks) return;
+  const int64_t c = (wb + kSpWaves - 1) / kSpWaves;
+  if (c * kBlockPos / a.P + 1 > 64) return;  // a split's page ids must fit the 64 lanes
+  const int64_t S = (blk + c - 1) / c;       // splits per sequence
+  // the narrowest workgroup (most workgroups, spread over the most CUs)
+  // whose sequence still leaves at most kSpMergeTrip partials, which the
+  // last workgroup reads in one trip
+  int nw = 2;
+  while (nw < 8 && (S + nw - 1) / nw > kSpMergeTrip) nw *= 2;
+  if (MK_ATTN_SP_NW) nw = MK_ATTN_SP_NW;
+  while (nw > 1 && nw / 2 >= S) nw /= 2;
+  while (nw > 1 && sp_lds_bytes(a, nw, D) > 65536) nw /= 2;
+  a.sp_blk = (int)c;
+  a.sp_nw = nw;
+  a.sp_nwg = (int)((S + nw - 1) / nw);
+}
+
+// Partial slots of the stream plan: pair + sequence < max_pairs + B.
 inline int64_t workspace_slots(const PagedArgs& a) { return (int64_t)a.max_pairs + a.B; }
 
-// Workspace: [O partials, slots * Hq * D fp32][(m, l), slots * Hq * 2 fp32]
+// Workspace: [arrival counters, kCounterBytes][O partials fp32][(m, l) fp32].
+// The counters sit at the same place for every shape (the short-context
+// plan has at most kSpMaxWaveBlocks of them); the partials are
+// slots * Hq * (D + 2) floats for the stream plan and B * Hq * sp_nwg * (D + 2)
+// for the short-context plan.
+constexpr size_t kCounterBytes = (size_t)kSpMaxWaveBlocks * sizeof(int);
 inline size_t workspace_need(const PagedArgs& a, int64_t D) {
-  return (size_t)workspace_slots(a) * a.Hq * (D + 2) * sizeof(float);
+  const int64_t stream_rows = workspace_slots(a) * a.Hq;
+  const int64_t sp_rows = a.sp_nw ? (int64_t)a.B * a.Hq * a.sp_nwg : 0;
+  const int64_t rows = stream_rows > sp_rows ? stream_rows : sp_rows;
+  return kCounterBytes + (size_t)rows * (D + 2) * sizeof(float);
 }
 
 int attention_launch(PagedArgs a, int64_t D, int kvf, int dtype, size_t ws_bytes,
@@ -1306,8 +1638,40 @@ int attention_launch(PagedArgs a, int64_t D, int kvf, int dtype, size_t ws_bytes
     a.lgP = ilog2(a.P);
     a.lg_gs = kvf ? ilog2(a.gs) : 0;
     split_plan(a, kvf);
+    sp_plan(a, D);
     const size_t need = workspace_need(a, D);
     if (!a.ws || ws_bytes < need || !mk_aligned(a.ws, 16)) return MK_ERR_INVALID;
+    a.cnt = reinterpret_cast<int*>(a.ws);
+    a.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.ws) + kCounterBytes);
+    if (a.sp_nw) {
+      a.ws_ml = a.ws + (size_t)a.B * a.Hq * a.sp_nwg * D;
+      const dim3 grid((unsigned)((int64_t)a.sp_nwg * a.B * a.units));
+      const dim3 block(64u * (unsigned)a.sp_nw);
+      const size_t lds = sp_lds_bytes(a, a.sp_nw, D);
+#define MK_SP(AT, DD, KF, SB) paged_attn_sp_kernel<AT, DD, KF, SB><<<grid, block, lds, st>>>(a)
+      if (kvf == 0) {
+        if (dtype == MK_DT_F16) {
+          if (D == 128) MK_SP(f16, 128, 0, false); else MK_SP(f16, 64, 0, false);
+        } else {
+          if (D == 128) MK_SP(bf16, 128, 0, false); else MK_SP(bf16, 64, 0, false);
+        }
+      } else if (kvf == 8) {
+        if (D == 128) {
+          if (a.gs >= 16) MK_SP(f16, 128, 8, true); else MK_SP(f16, 128, 8, false);
+        } else {
+          if (a.gs >= 16) MK_SP(f16, 64, 8, true); else MK_SP(f16, 64, 8, false);
+        }
+      } else {
+        if (D == 128) {
+          if (a.gs >= 32) MK_SP(f16, 128, 4, true); else MK_SP(f16, 128, 4, false);
+        } else {
+          if (a.gs >= 16) MK_SP(f16, 64, 4, true); else MK_SP(f16, 64, 4, false);
+        }
+      }
+#undef MK_SP
+      MK_CHECK_LAUNCH();
+      return MK_OK;
+    }
     a.ws_ml = a.ws + (size_t)workspace_slots(a) * a.Hq * D;
     const dim3 grid((unsigned)((int64_t)a.max_pairs * (a.units / a.wg_units)));
     const dim3 block(64u * (unsigned)a.wg_units);
@@ -1447,6 +1811,7 @@ size_t mk_paged_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, in
   a.P = (int)page_size;
   a.MB = (int)max_blocks;
   split_plan(a, 0);  // the workspace does not depend on the format
+  sp_plan(a, D);
   return workspace_need(a, D);
 }
 
@@ -1477,6 +1842,7 @@ int mk_paged_decode_attention_noalloc(const void* q, const void* K_pages, const 
   if (fast_ok(D, 0, dtype, a.gs, a.P, a.NP, a.Hkv)) {
     PagedArgs plan = a;
     split_plan(plan, 0);
+    sp_plan(plan, D);
     if (workspace_need(plan, D) > kNoAllocScratchBytes) return MK_ERR_SCRATCH;
   }
   void* ws = nullptr;

@@ -179,11 +179,38 @@ def workspace_bytes(B: int, Hq: int, Hkv: int, D: int, max_blocks: int, page_siz
     return int(load().mk_paged_attention_workspace_bytes(B, Hq, Hkv, D, max_blocks, page_size))
 
 
+# Zero-filled paged-attention workspaces, one per (device, stream).  The
+# library keeps arrival counters at the start of the workspace: they must be
+# zero before a call and every call leaves them zero, so one buffer serves
+# every call issued on its stream (calls on one stream never overlap).
+# A graph captured on a stream keeps using the buffer that stream had at
+# capture time, so a replaced buffer is retired (kept alive), never freed.
+_WORKSPACES: dict = {}
+_RETIRED: list = []
+_WS_LOCK = threading.Lock()
+
+
 def attention_workspace(device: torch.device, B: int, Hq: int, Hkv: int, D: int, max_blocks: int,
                         page_size: int):
-    """(scratch, nbytes) for one paged-attention call: split partials, no
-    initial contents needed (None when the call needs none)."""
+    """(workspace, nbytes) for one paged-attention call on the current stream
+    of ``device``: the stream's zero-filled workspace, replaced by a larger
+    one when the call needs more.  Under graph capture with no large enough
+    buffer cached, a new zero-filled buffer is made for the captured call
+    (the graph then zero-fills it on every replay)."""
     nbytes = workspace_bytes(B, Hq, Hkv, D, max_blocks, page_size)
     if nbytes <= 0:
         return None, 0
-    return torch.empty((nbytes + 15) // 16 * 16, dtype=torch.uint8, device=device), nbytes
+    size = (nbytes + 15) // 16 * 16
+    dev = torch.device(device)
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    with _WS_LOCK:
+        buf = _WORKSPACES.get(key)
+        if buf is not None and buf.numel() >= size:
+            return buf, nbytes
+        old = buf
+        buf = torch.zeros(size, dtype=torch.uint8, device=dev)
+        if not torch.cuda.is_current_stream_capturing():
+            if old is not None:
+                _RETIRED.append(old)
+            _WORKSPACES[key] = buf
+    return buf, nbytes

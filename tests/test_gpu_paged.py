@@ -76,6 +76,22 @@ def test_paged_update_collision_later_b_wins(dev):
 
 # ------------------------------------------------------------ fp16 paged attention
 
+# The short-context plan runs while B x 32-position blocks per table row x
+# units (kv heads x blocks of 16 query heads) is at most this; its arrival
+# counters (4 bytes each) lead the workspace.
+SP_MAX_WAVE_BLOCKS = 16384
+
+
+def _pad_table(bt, NP, width, seed):
+    """The block table widened to ``width`` pages per sequence with random
+    valid page ids past the used ones: a wide table moves the attention from
+    the short-context plan (laid out from the table width) to the stream
+    plan without changing the result."""
+    extra = np.random.default_rng(seed).integers(0, NP, size=(bt.shape[0], width - bt.shape[1]))
+    return np.concatenate([bt, extra.astype(np.int32)], axis=1)
+
+
+
 ATTN_CASES = [
     # (B, Hq, Hkv, D, P, max_blocks)   fast path D in {64,128}; generic otherwise
     (2, 4, 4, 64, 4, 8),
@@ -144,17 +160,22 @@ def test_paged_attention_pairs_at_block_cap(dev):
     assert_close(got, ref, rtol=1e-2, atol=1e-3, what="long context")
 
 
+@pytest.mark.parametrize("wide", [False, True])
 @pytest.mark.parametrize("lengths", [[64], [2047], [2048], [2049], [95, 1, 2000], [8191], [8224]])
-def test_paged_attention_short_context_split(dev, lengths):
-    """A short total context shortens the pairs of the stream plan (down to two
-    32-position blocks) so that 32 of them run; the block totals straddle the
-    points where that minimum changes (64 and 256 blocks), and a single pair
-    covering its whole sequence is written without the merge."""
+def test_paged_attention_short_context_split(dev, lengths, wide):
+    """Short total contexts.  With the table as wide as the longest sequence
+    they take the short-context plan (one, two or three blocks per split,
+    one or several workgroups per sequence).  With a wide table they take the
+    stream plan, whose pairs shorten (down to two 32-position blocks) so that
+    32 of them run; the block totals straddle the points where that minimum
+    changes (64 and 256 blocks), and a single pair covering its whole sequence
+    is written without the merge."""
     B, Hq, Hkv, D, P = len(lengths), 32, 8, 128, 16
     mb = (max(lengths) + P - 1) // P
     q, Kp, Vp, bt, lengths = _case(31 + sum(lengths), B, Hq, Hkv, D, P, mb, lengths=lengths)
+    btw = _pad_table(bt, Kp.shape[0], max(mb, SP_MAX_WAVE_BLOCKS * 32 // (B * 8 * P) + 2), 10) if wide else bt
     qt, Kt, Vt = (_t(a, dev, torch.float16) for a in (q, Kp, Vp))
-    got = gqa.paged_gqa_decode_attention(qt[:, None], Kt, Vt, to_dev(bt, dev), to_dev(lengths, dev))[:, 0]
+    got = gqa.paged_gqa_decode_attention(qt[:, None], Kt, Vt, to_dev(btw, dev), to_dev(lengths, dev))[:, 0]
     ref = op.paged_attention(qt.float().cpu().numpy(), Kt.float().cpu().numpy(), Vt.float().cpu().numpy(), bt,
                              lengths)
     assert_close(got, ref, rtol=1e-2, atol=1e-3, what=f"short context {lengths.tolist()}")
@@ -221,6 +242,64 @@ def test_paged_decode_attention_mha(dev, backend):
     assert_close(got[:, 0], ref, what=backend)
     with pytest.raises(ValueError, match="metal_d128"):
         pk.paged_decode_attention(qt[:, None], Kt, Vt, to_dev(bt, dev), lengths.tolist(), backend="metal_d128")
+
+
+STREAM_CASES = [
+    # (B, Hq, Hkv, D, P, used pages, lengths or None)
+    (2, 32, 8, 128, 16, 40, None),
+    (3, 24, 12, 128, 16, 30, None),
+    (2, 32, 1, 64, 32, 12, None),
+    (2, 8, 2, 128, 64, 40, None),
+    (70, 8, 2, 128, 16, 8, [0, 1, 5, 31, 32, 33, 0, 2, 64, 17, 0, 0, 3, 100] * 5),
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,P,mb,lengths", STREAM_CASES)
+def test_paged_attention_stream_plan(dev, B, Hq, Hkv, D, P, mb, lengths):
+    """Shapes the short-context plan would take, run on the stream plan through
+    a block table wide enough (B x 32-position blocks x units > SP_MAX_WAVE_BLOCKS)."""
+    q, Kp, Vp, bt, lengths = _case(200 + B + D, B, Hq, Hkv, D, P, mb, lengths=lengths)
+    units = Hkv * ((Hq // Hkv + 15) // 16)
+    width = max(mb, -(-(SP_MAX_WAVE_BLOCKS + 1) * 32 // (B * units * P)) + 1)
+    btw = _pad_table(bt, Kp.shape[0], width, 9)
+    qt, Kt, Vt = (_t(a, dev, torch.float16) for a in (q, Kp, Vp))
+    got = gqa.paged_gqa_decode_attention(qt[:, None], Kt, Vt, to_dev(btw, dev), to_dev(lengths, dev))[:, 0]
+    ref = op.paged_attention(qt.float().cpu().numpy(), Kt.float().cpu().numpy(), Vt.float().cpu().numpy(), bt,
+                             lengths)
+    assert_close(got, ref, rtol=1e-2, atol=1e-3, what=f"stream plan B{B} Hq{Hq} Hkv{Hkv} D{D} P{P}")
+
+
+def _counters_zero(dev):
+    from mk import _lib
+    buf = _lib._WORKSPACES[(torch.device(dev).index, torch.cuda.current_stream(dev).cuda_stream)]
+    return bool(torch.all(buf[:4 * SP_MAX_WAVE_BLOCKS] == 0).item())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_paged_attention_short_plan_calls_in_a_row(dev, dtype):
+    """Short-context plan: sequences spread over several workgroups merge
+    through the arrival counters, which every call leaves at zero -- calls in
+    a row on one workspace, with other lengths and other shapes between, all
+    match the oracle, and the counters read zero after each."""
+    cases = [
+        (1, 32, 8, 128, 16, 137, [2049]),          # B = 1 decode at ~2k: one block per split
+        (1, 32, 8, 128, 16, 137, [2176]),
+        (1, 32, 8, 128, 16, 512, [8192]),           # one 8k sequence
+        (4, 32, 8, 128, 16, 137, [2049, 33, 2176, 1000]),  # two blocks per split
+        (3, 32, 8, 128, 16, 512, [4096, 8192, 31]),  # three blocks per split
+        (2, 32, 8, 64, 32, 64, [2048, 1]),
+        (16, 32, 8, 128, 16, 137, [2100 - 7 * i for i in range(16)]),  # five blocks per split
+        (1, 32, 8, 128, 16, 137, [2049]),
+    ]
+    for i, (B, Hq, Hkv, D, P, mb, lengths) in enumerate(cases):
+        q, Kp, Vp, bt, ln = _case(300 + i, B, Hq, Hkv, D, P, mb, lengths=lengths)
+        qt, Kt, Vt = (_t(a, dev, dtype) for a in (q, Kp, Vp))
+        got = gqa.paged_gqa_decode_attention(qt[:, None], Kt, Vt, to_dev(bt, dev), to_dev(ln, dev))[:, 0]
+        ref = op.paged_attention(qt.float().cpu().numpy(), Kt.float().cpu().numpy(), Vt.float().cpu().numpy(),
+                                 bt, ln)
+        tol = (1e-2, 1e-3) if dtype == torch.float16 else (3e-2, 4e-3)
+        assert_close(got, ref, rtol=tol[0], atol=tol[1], what=f"call {i}: B{B} D{D} lengths {lengths}")
+        assert _counters_zero(dev), f"arrival counters left non-zero after call {i}"
 
 
 def test_config3_full_size(dev):
