@@ -1390,30 +1390,37 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   lds_barrier();
   if (!is_last) return;
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  // tp consecutive threads share an output chunk (4 floats of one head),
+  // each taking every tp-th partial, 16 per trip, all requested before any is
+  // used; a trip that raises a thread's max rescales its running (M, L, O),
+  // and the tp running states are combined by lane shuffles at the end
   constexpr int DV = D / 4;  // 4-float chunks per head row
-  for (int it = threadIdx.x; it < hcount * DV; it += blockDim.x) {
+  constexpr int CH = kSpMergeTrip;
+  const int items = hcount * DV;
+  int tp = 1;
+  while (tp < 8 && items * tp * 2 <= (int)blockDim.x && nwg > CH * tp) tp *= 2;
+  const int sub = (int)threadIdx.x & (tp - 1);
+  for (int it = (int)threadIdx.x / tp; it < items; it += (int)blockDim.x / tp) {
     const int h = it / DV;
     const int dv = it - h * DV;
     const size_t row0 = prow + (size_t)h * a.sp_nwg;
     const f32x2* ml = reinterpret_cast<const f32x2*>(a.ws_ml) + row0;
     const f32x4* po = reinterpret_cast<const f32x4*>(a.ws + row0 * D) + dv;  // partial g at po[g * DV]
-    // 16 partials per trip, all requested before any is used; the running
-    // (M, L, O) is rescaled when a trip raises the max
-    constexpr int CH = kSpMergeTrip;
     float M = -INFINITY, L = 0.0f;
     float O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int g0 = 0; g0 < nwg; g0 += CH) {
+    for (int g0 = sub; g0 < nwg; g0 += CH * tp) {
       f32x2 v[CH];
       f32x4 x[CH];
 #pragma unroll
       for (int k = 0; k < CH; ++k) {
-        const int g = g0 + k < nwg ? g0 + k : nwg - 1;  // past the end: re-read, weight 0
+        const int gk = g0 + k * tp;
+        const int g = gk < nwg ? gk : nwg - 1;  // past the end: re-read, weight 0
         v[k] = ml[g];
         x[k] = po[(size_t)g * DV];
       }
       float Mc = M;
 #pragma unroll
-      for (int k = 0; k < CH; ++k) Mc = fmaxf(Mc, g0 + k < nwg ? v[k][0] : -INFINITY);
+      for (int k = 0; k < CH; ++k) Mc = fmaxf(Mc, g0 + k * tp < nwg ? v[k][0] : -INFINITY);
       const float Mu = Mc == -INFINITY ? 0.0f : Mc;
       const float r = __builtin_amdgcn_exp2f(M - Mu);  // 0 while M is -inf
       L *= r;
@@ -1421,16 +1428,32 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       for (int e = 0; e < 4; ++e) O[e] *= r;
 #pragma unroll
       for (int k = 0; k < CH; ++k) {
-        const float w = g0 + k < nwg ? __builtin_amdgcn_exp2f(v[k][0] - Mu) : 0.0f;
+        const float w = g0 + k * tp < nwg ? __builtin_amdgcn_exp2f(v[k][0] - Mu) : 0.0f;
         L += v[k][1] * w;
 #pragma unroll
         for (int e = 0; e < 4; ++e) O[e] += x[k][e] * w;
       }
       M = Mc;
     }
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    *reinterpret_cast<u32x2*>(out + h * D + 4 * dv) =
-        (u32x2){pack_act2<AT>(O[0] * inv, O[1] * inv), pack_act2<AT>(O[2] * inv, O[3] * inv)};
+    for (int off = tp >> 1; off > 0; off >>= 1) {  // tp is uniform
+      const float Mo = __shfl_xor(M, off, 64);
+      const float Lo = __shfl_xor(L, off, 64);
+      float Oo[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Oo[e] = __shfl_xor(O[e], off, 64);
+      const float Mn = fmaxf(M, Mo);
+      const float Mu = Mn == -INFINITY ? 0.0f : Mn;
+      const float r0 = __builtin_amdgcn_exp2f(M - Mu), r1 = __builtin_amdgcn_exp2f(Mo - Mu);
+      L = L * r0 + Lo * r1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) O[e] = O[e] * r0 + Oo[e] * r1;
+      M = Mn;
+    }
+    if (sub == 0) {
+      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+      *reinterpret_cast<u32x2*>(out + h * D + 4 * dv) =
+          (u32x2){pack_act2<AT>(O[0] * inv, O[1] * inv), pack_act2<AT>(O[2] * inv, O[3] * inv)};
+    }
   }
 }
 
