@@ -42,7 +42,7 @@ TRAFFIC_SUMMARY = "gemv_dot_q4_rmsnorm_gate_up_M1_traffic.json"
 ATTN_TRAFFIC_SUMMARY = "paged_attn_config3_fp16_traffic.json"
 
 
-WORKLOADS = ("config3", "config4", "mlp_m4", "mlp_m8", "mlp_m32", "mlp_q8", "stack")
+WORKLOADS = ("config3", "attn_short", "config4", "mlp_m4", "mlp_m8", "mlp_m32", "mlp_q8", "stack")
 
 
 def _parse():
@@ -57,7 +57,8 @@ def _parse():
                     help="run only the config-5 decode stack extra and print its JSON (same as --workload stack)")
     ap.add_argument("--workload", choices=WORKLOADS, default=None,
                     help="run one workload alone and print its JSON (for profiling): config3 (paged fp16 "
-                         "attention), config4 (q8/q4 KV attention), mlp_m4 / mlp_m8 / mlp_m32 (batched q4 MLP "
+                         "attention), attn_short (fp16 attention at B=1 2k / 8k and B=4 2k), config4 (q8/q4 KV "
+                         "attention), mlp_m4 / mlp_m8 / mlp_m32 (batched q4 MLP "
                          "steps), mlp_q8 (q8 MLP step, M=1), stack (config-5 decode stack)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="first run a plain device copy of this many MiB (counter calibration)")
@@ -249,6 +250,43 @@ def attention_config3(dev, steps, warmup):
                      "kernel": "paged_attn_kernel<f16,128,0,false,true> + paged_attn_merge_kernel<f16,128>",
                      "bytes_per_launch": nbytes, "us_per_launch": round(ms * 1e3, 3)},
     }
+
+
+def attention_short(dev, steps=200, warmup=20):
+    """Short total contexts (the one-kernel short-context plan): one sequence
+    of 2048 and of 8192 positions, and four of ~2k -- Hq 32 / Hkv 8, D=128,
+    P=16, fp16 K/V ~ N(0,1), a seeded permuted block table as wide as the
+    longest sequence.  Enough cache copies rotate through the calls (>= 256 MB
+    in all) that every call reads its K/V from HBM, as a decode step does
+    after the other layers' traffic."""
+    import numpy as np
+    import torch
+
+    import mk.gqa_ops as gqa
+
+    Hq, Hkv, D, P = 32, 8, 128, 16
+    out = {}
+    for name, lengths in (("B1_ctx2048", [2048]), ("B1_ctx8192", [8192]), ("B4_ctx2048", [2048, 2049, 2100, 2176])):
+        B = len(lengths)
+        mb = -(-max(lengths) // P)
+        NP = B * mb
+        bt = torch.from_numpy(np.random.default_rng(4).permutation(NP).astype(np.int32).reshape(B, mb)).to(dev)
+        ln = torch.tensor(lengths, dtype=torch.int32, device=dev)
+        q = torch.randn((B, 1, Hq, D), device=dev).to(torch.float16)
+        copy_bytes = NP * P * Hkv * D * 2 * 2
+        ncopy = max(2, -(-(256 << 20) // copy_bytes))
+        caches = [(torch.randn((NP, P, Hkv, D), device=dev).to(torch.float16),
+                   torch.randn((NP, P, Hkv, D), device=dev).to(torch.float16)) for _ in range(ncopy)]
+        fns = [lambda K=K, V=V: gqa.paged_gqa_decode_attention(q, K, V, bt, ln) for K, V in caches]
+        ms = time_steps(fns, max(steps, ncopy), warmup)
+        tot = int(sum(lengths))
+        nbytes = tot * Hkv * D * 2 * 2 + sum(-(-n // P) for n in lengths) * 4 + B * Hq * D * 2 * 2 + B * 4
+        achieved = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us_per_call": round(ms * 1e3, 3), "bytes": nbytes, "hbm_gbs": round(achieved, 1),
+                     "frac_of_peak": round(achieved / PEAK_GBS, 4), "cache_copies": ncopy}
+        del caches, fns
+        torch.cuda.empty_cache()
+    return out
 
 
 def attention_config4(dev, steps=30, warmup=5):
@@ -623,6 +661,8 @@ def run_workload(name, dev, args):
         return attention_config3(dev, max(50, args.steps // 3), 10)
     if name == "config4":
         return attention_config4(dev)
+    if name == "attn_short":
+        return {"workload": "paged_gqa_fp16_short_contexts", **attention_short(dev)}
     if name == "stack":
         return decode_stack_config5(dev)
     sets = [make_mlp_set(dev, 4, 100 + i) for i in range(args.sets)]
@@ -695,6 +735,7 @@ def main():
             extra[f"q{bits}_mlp_M{M}"] = mlp_extra(dev, sets, M, bits, max(60, args.steps // 3))
         torch.cuda.empty_cache()
         extra["paged_attention"] = attention_config3(dev, max(50, args.steps // 3), 10)
+        extra["paged_attention_short"] = attention_short(dev)
         extra["quantized_attention"] = attention_config4(dev)
         extra["decode_stack"] = decode_stack_config5(dev)
 
