@@ -69,6 +69,8 @@ def _parse():
     ap.add_argument("--summary-kernel", default=DOMINANT_KERNEL,
                     help="kernel-name substring the traffic summary is for (default: the MLP front kernel)")
     ap.add_argument("--summary-workload", default="config2 residual+RMSNorm+gate/up 2x14336x4096 q4 g64 M=1")
+    ap.add_argument("--summary-grid", type=int, default=0,
+                    help="with --summarize-counters: only attention dispatches of this grid size (threads)")
     ap.add_argument("--summary-bytes", type=int, default=0,
                     help="algorithmic bytes per launch of that kernel (default: the MLP front's)")
     ap.add_argument("--summarize-pmc", nargs=4, metavar=("CSV", "OUT_MD", "TITLE", "COMMAND"),
@@ -502,20 +504,26 @@ def _counter_rows(path, counter):
 READ_REQ_COUNTERS = ("TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_128B_sum")
 
 
-def _dispatch_bytes(path, counter):
+def _dispatch_bytes(path, counter, grid=0):
     """(kernel name, bytes) per dispatch: from WRITE_SIZE / FETCH_SIZE (KiB),
     or for reads from the L2->fabric request counts by size
     (32 n32 + 64 n64 + 128 n128; the FETCH_SIZE expression reads 128-byte
-    requests through TCC_BUBBLE, which does not always count them)."""
+    requests through TCC_BUBBLE, which does not always count them).  A
+    non-zero ``grid`` keeps only the attention dispatches of that grid size
+    (threads), so workloads that launch one kernel at several sizes can be
+    told apart."""
     import csv
 
     per = {}
     with open(path, newline="") as f:
         for r in csv.DictReader(f):
-            d = per.setdefault(r["Dispatch_Id"], {"kernel": r.get("Kernel_Name", "")})
+            d = per.setdefault(r["Dispatch_Id"], {"kernel": r.get("Kernel_Name", ""),
+                                                  "grid": int(r.get("Grid_Size") or 0)})
             d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
     out = []
     for d in per.values():
+        if grid and d["grid"] != grid and "gemv" not in d["kernel"] and "paged" in d["kernel"]:
+            continue
         if counter in d:
             out.append((d["kernel"], d[counter] * 1024.0))
         elif counter == "FETCH_SIZE" and "TCC_EA0_RDREQ_128B_sum" in d:
@@ -525,7 +533,7 @@ def _dispatch_bytes(path, counter):
 
 
 def summarize_counters(fetch_csv, write_csv, out_path, copy_mb, kernel=DOMINANT_KERNEL, workload=None,
-                       algo_bytes=0):
+                       algo_bytes=0, grid=0):
     """HBM traffic per launch of ``kernel``: reads from one --pmc pass
     (FETCH_SIZE, or the read-request counts by size), writes from a WRITE_SIZE
     pass.  The plain copy of ``copy_mb`` MiB run by --calib-copy-mb reads and
@@ -534,7 +542,7 @@ def summarize_counters(fetch_csv, write_csv, out_path, copy_mb, kernel=DOMINANT_
     copy_bytes = copy_mb * (1 << 20)
     out = {"kernel": kernel, "workload": workload, "algorithmic_bytes": None, "copy_bytes": copy_bytes}
     for name, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
-        rows = _dispatch_bytes(path, name)
+        rows = _dispatch_bytes(path, name, grid)
         dom = [v for k, v in rows if kernel in _demangled(k)]
         # the calibration copy: copy-kernel dispatches whose count is nearest
         # the copy's size
@@ -690,7 +698,8 @@ def main():
         return
     if args.summarize_counters:
         summarize_counters(*args.summarize_counters, args.summary_out, args.calib_copy_mb or 256,
-                           kernel=args.summary_kernel, workload=args.summary_workload, algo_bytes=args.summary_bytes)
+                           kernel=args.summary_kernel, workload=args.summary_workload, algo_bytes=args.summary_bytes,
+                           grid=args.summary_grid)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one GPU; multi-GPU runs are not part of it",
