@@ -771,6 +771,7 @@ __global__ __launch_bounds__(1024) void gemv_xs_kernel(const GemvArgs args) {
   const f16* sbase = reinterpret_cast<const f16*>((sp & 1) && has_z ? args.z[sp >> 1] : args.s[sp >> 1]) +
                      (size_t)srow * G + 8 * sc8;
   const uint32_t code_off = (uint32_t)r * (uint32_t)args.row_bytes + (uint32_t)(ka >> 1);
+  __shared__ int rk_slots[EPI == EPI_ROPE_KV ? kRopeRows : 1];  // EPI_ROPE_KV: the rows' cache slots
 
   // the activation block: column 16 mt + r (rows past M repeat row M - 1;
   // their results are dropped)
@@ -847,10 +848,15 @@ __global__ __launch_bounds__(1024) void gemv_xs_kernel(const GemvArgs args) {
       }
       const int nb = t * 16 + 4 * kb;
       if (m < M && t < t_end) {
+        if constexpr (EPI == EPI_ROPE_KV) {  // NMAT == 1; the pairs are (nb, nb+1), (nb+2, nb+3)
+          rope_kv_pair(args, rk_slots, m, nb, v[0][0], v[0][1]);
+          rope_kv_pair(args, rk_slots, m, nb + 2, v[0][2], v[0][3]);
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int nn = nb + i;
-          if (nn < N) store_out<f16, EPI>(args, (size_t)m * N + nn, v[0][i], v[NMAT - 1][i]);
+          for (int i = 0; i < 4; ++i) {
+            const int nn = nb + i;
+            if (nn < N) store_out<f16, EPI>(args, (size_t)m * N + nn, v[0][i], v[NMAT - 1][i]);
+          }
         }
       }
     }
@@ -866,6 +872,9 @@ __global__ __launch_bounds__(1024) void gemv_xs_kernel(const GemvArgs args) {
   // loop refills the same registers in place every iteration, so no buffer
   // is copied across it.  The steps for a tile past the run compute on
   // re-read data and store nothing.
+  // EPI_ROPE_KV: the rows' cache slots, in LDS before the first barrier
+  if constexpr (EPI == EPI_ROPE_KV) rope_fill_slots(args, rk_slots);
+
   Buf b;
   issue(t_begin, b);
   __builtin_amdgcn_sched_barrier(0);
@@ -1253,17 +1262,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
   const int u = ubase + lane;
   const int k0 = (u < U ? u : 0) * 32;
   if constexpr (NORM) {
+    // chunks past the row (threads beyond K / 8, which the norm below
+    // leaves out) re-read chunk 0, so every load stays inside the row
     const int c0 = threadIdx.x, c1 = two ? threadIdx.x + nthr : threadIdx.x;
-    const int c1c = c1 < nchunk ? c1 : c0;
+    const int c0c = c0 < nchunk ? c0 : 0;
+    const int c1c = c1 < nchunk ? c1 : c0c;
     // no residual: the loads read x again and are dropped, so every load
     // still issues in order
     const f16* rp = reinterpret_cast<const f16*>(args.nres ? args.nres : args.x);
     const f16* wp = reinterpret_cast<const f16*>(args.nw);
-    ax[0] = ldg128(x + 8 * c0);
+    ax[0] = ldg128(x + 8 * c0c);
     ax[1] = ldg128(x + 8 * c1c);
-    ar[0] = ldg128(rp + 8 * c0);
+    ar[0] = ldg128(rp + 8 * c0c);
     ar[1] = ldg128(rp + 8 * c1c);
-    aw[0] = ldg128(wp + 8 * c0);
+    aw[0] = ldg128(wp + 8 * c0c);
     aw[1] = ldg128(wp + 8 * c1c);
     if (!args.nres) ar[0] = ar[1] = (u32x4){0u, 0u, 0u, 0u};
     __builtin_amdgcn_sched_barrier(0);
@@ -1604,10 +1616,11 @@ inline int gemv_device_cus() {
 }
 
 // the activation-stationary kernel takes 5..32-row batches of matrices with at
-// least this many 16-row tiles (fewer tiles than about two per CU leave the
-// per-workgroup activation load unamortised)
+// least this many 16-row tiles, one per CU (measured against the K-split
+// kernel at 8 / 16 / 32 rows, us: 4096 x 4096 7.05 / 8.2 / 12.8 against 7.5 /
+// 8.65 / 13.0; 6144 x 4096 9.1 / 10.3 / 14.9 against 13.0 / 15.3 / 24.4)
 constexpr int kXsMinRows = 5;
-constexpr int kXsMinTiles = 512;
+constexpr int kXsMinTiles = 256;
 constexpr size_t kXsMaxLds = 160 * 1024;
 
 // K-split launch: one 16-row tile per workgroup of 16 waves
@@ -1662,7 +1675,7 @@ int launch_xs(GemvArgs a, hipStream_t st) {
 // aligned x and codes, and enough rows that every CU gets tiles to stream
 template <int BITS, int NMAT, int EPI>
 bool xs_eligible(const GemvArgs& a, int mt, int act_dt, int sc_dt) {
-  bool ok = BITS == 4 && EPI != EPI_ROPE_KV && act_dt == MK_DT_F16 && sc_dt == MK_DT_F16 && a.lg >= 5 &&
+  bool ok = BITS == 4 && (EPI != EPI_ROPE_KV || NMAT == 1) && act_dt == MK_DT_F16 && sc_dt == MK_DT_F16 && a.lg >= 5 &&
             (a.K % 256) == 0 && a.K >= 256 && a.K <= 4096 &&
             (a.N % 16) == 0 && a.N / 16 >= kXsMinTiles && mk_aligned(a.x, 16) && (size_t)a.row_bytes % 16 == 0 &&
             (a.G % 8) == 0 && 4 * NMAT * a.G <= 64 * (a.K / 256) &&  // one (s, z) vector per thread
@@ -1811,7 +1824,7 @@ int gemv_dispatch(GemvArgs a, int64_t M, int64_t N, int64_t K, int64_t gs, int a
   }
   int64_t m_done = 0;
   // up to 32 rows at a time through the activation-stationary kernel
-  if constexpr (EPI != EPI_ROPE_KV) {
+  {
     if (M >= kXsMinRows && xs_eligible<BITS, NMAT, EPI>(a, 1, act_dt, sc_dt)) {
       while (M - m_done >= kXsMinRows && rc == MK_OK) {
         GemvArgs b = a;

@@ -46,12 +46,13 @@ def _np_layer(rng):
             "ln2": (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float16)}
 
 
-@pytest.mark.parametrize("B", [1, 32])
+@pytest.mark.parametrize("B", [1, 8, 32])
 def test_fused_front_full_shape_bit_exact(dev, B):
     """RMSNorm (K = 4096) + 6144-row qkv projection + D = 128 RoPE pairs +
     paged write, fused, against norm + projection + mk_qkv_rope_paged_update:
-    q and every cache byte equal (batch 1: one launch; batch 32: norm kernel +
-    two-column tile projection with the RoPE epilogue)."""
+    q and every cache byte equal (batch 1: one launch; batch 8 / 32: norm
+    kernel + the activation-stationary projection with the RoPE epilogue, one
+    and two 16-column tiles)."""
     rng = np.random.default_rng(500 + B)
     print(f"fused front full shape B={B}", flush=True)
     cfg = _cfg()
