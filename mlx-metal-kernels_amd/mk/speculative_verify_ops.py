@@ -37,18 +37,6 @@ from .paged_quantized_kv_ops import PagedQuantizedKVCache, _hip_quantized_attent
 
 _ACT = (torch.float16, torch.bfloat16)
 
-# The HIP verify paths are switched off: runs of their GPU tests ended in a GPU
-# memory fault whose cause has not been found (every kernel they launch checks
-# in bounds for those shapes when its address arithmetic is replayed on the
-# host), so until it is, they raise instead of launching.  The reference
-# backend (torch ops) runs.
-_HIP_VERIFY_DISABLED = ("the HIP speculative-verify path is disabled pending the cause of a GPU memory fault seen "
-                        "in its tests; use backend='reference'")
-
-
-def _hip_verify_off():
-    raise RuntimeError(_HIP_VERIFY_DISABLED)
-
 
 # ------------------------------------------------------------ config / result
 
@@ -256,7 +244,6 @@ def paged_verify_attention(q, K_pages, V_pages, block_table, lengths=None, scale
         raise TypeError(f"K_pages dtype must be float16 or bfloat16, got {K_pages.dtype}")
     if q.shape[3] != K_pages.shape[3] or q.shape[2] % K_pages.shape[2]:
         raise ValueError(f"q {tuple(q.shape)} does not fit pages {tuple(K_pages.shape)}")
-    _hip_verify_off()
     sc = 1.0 / math.sqrt(q.shape[3]) if scale is None else scale
     rows_bt, rows_len = _row_tables(block_table, torch.clamp(ln, max=max_s), W)
     B, W, Hq, D = q.shape
@@ -277,7 +264,6 @@ def paged_quantized_verify_attention(q, paged_qkv: PagedQuantizedKVCache, length
         return reference_paged_verify_attention(q, Kp.to(q.dtype), Vp.to(q.dtype), paged_qkv.block_table, ln, sc)
     if backend.lower() not in ("auto", "metal"):
         raise ValueError("backend must be one of 'reference', 'metal', 'auto'")
-    _hip_verify_off()
     import dataclasses
 
     rows_bt, rows_len = _row_tables(paged_qkv.block_table, torch.clamp(ln, max=max_s), W)
@@ -325,7 +311,6 @@ def llama_stack_verify_step(x, stack_weights: LlamaStackWeights, stack_cache: Ll
         raise ValueError(f"x must have shape [B,W,{config.hidden_size}], got {tuple(x.shape)}")
     B, W, H = x.shape
     dev = _lib.require_device(x)
-    _hip_verify_off()
     p0 = normalize_positions(position, B, stack_cache.max_seq_len - W + 1, device=dev).to(torch.int32)
     pos_rows = (p0[:, None] + torch.arange(W, dtype=torch.int32, device=dev)[None, :]).reshape(B * W)
     res = llama_stack_decode_step(x.reshape(B * W, 1, H), stack_weights, _rows_cache(stack_cache, B, W), cos, sin,

@@ -17,9 +17,7 @@ from oracle import paged as op
 from tests._data import assert_close
 from tests.test_gpu_llama import _cfg, _linear, _np_layer, _t_layer
 
-pytestmark = [pytest.mark.gpu, pytest.mark.skip(
-    reason="the HIP verify path is switched off: two runs of these tests ended in a GPU memory fault whose cause "
-           "is not found yet (mk/speculative_verify_ops.py)")]
+pytestmark = pytest.mark.gpu
 
 
 def _pages(rng, B, mb, P, Hkv, D, extra=3):

@@ -86,7 +86,8 @@ def test_row_tables():
     assert np.array_equal(rows_len.numpy().reshape(2, 3), op.verify_row_lengths([10, 2], 3))
 
 
-def test_hip_verify_path_is_switched_off():
+def test_hip_verify_path_needs_a_device():
+    """The HIP verify attention refuses host tensors (no CPU fallback)."""
     q = torch.zeros(1, 2, 8, 64, dtype=torch.float16)
     K = torch.zeros(4, 16, 8, 64, dtype=torch.float16)
     bt = torch.zeros(1, 4, dtype=torch.int32)
