@@ -328,12 +328,15 @@ __device__ __forceinline__ void rope_kv_store(const GemvArgs& a, const int* slot
 }
 
 // EPI_ROPE_KV with both values of an (even n, n + 1) pair in one lane (the
-// MFMA kernels' output layout): the same arithmetic as rope_kv_store.
+// MFMA kernels' output layout): the same arithmetic as rope_kv_store.  RES:
+// slots[m] already holds the row's final slot (-1 when skipped or taken by a
+// later row) and pos_l[m] its position, both in LDS.
+template <bool RES = false>
 __device__ __forceinline__ void rope_kv_pair(const GemvArgs& a, const int* slots, int m, int n, float v0,
-                                             float v1) {
+                                             float v1, const int* pos_l = nullptr) {
   if (n >= a.N || m >= a.M) return;
   const RopeKV& r = a.rk;
-  const int p = r.pos[m];
+  const int p = RES ? pos_l[m] : r.pos[m];
   if (p < 0 || p >= r.cos_rows) return;
   const int D = r.D, QD = r.Hq * D, KD = r.Hkv * D;
   const int d = n % D;
@@ -358,11 +361,25 @@ __device__ __forceinline__ void rope_kv_pair(const GemvArgs& a, const int* slots
   } else {
     h = (n - QD - KD) / D;
   }
-  const int sl = rope_slot(a, slots, m);
+  const int sl = RES ? slots[m] : rope_slot(a, slots, m);
   if (sl < 0) return;
   f16* o = dst + (size_t)sl * KD + (size_t)h * D + d;
   o[0] = o0;
   o[1] = o1;
+}
+
+// The rows' final slots (the later-row-wins rule applied) and positions into
+// LDS: call after rope_fill_slots(a, raw) and a barrier; the values are
+// visible after the next barrier.
+__device__ __forceinline__ void rope_resolve_slots(const GemvArgs& a, const int* raw, int* res, int* pos_l) {
+  const int t = threadIdx.x;
+  if (t < a.M && t < kRopeRows) {
+    int sl = raw[t];
+    for (int b2 = t + 1; b2 < a.M; ++b2)
+      if (raw[b2] == sl) sl = -1;
+    res[t] = sl;
+    pos_l[t] = a.rk.pos[t];
+  }
 }
 
 // --------------------------------------------------------------------------
@@ -771,7 +788,11 @@ __global__ __launch_bounds__(1024) void gemv_xs_kernel(const GemvArgs args) {
   const f16* sbase = reinterpret_cast<const f16*>((sp & 1) && has_z ? args.z[sp >> 1] : args.s[sp >> 1]) +
                      (size_t)srow * G + 8 * sc8;
   const uint32_t code_off = (uint32_t)r * (uint32_t)args.row_bytes + (uint32_t)(ka >> 1);
-  __shared__ int rk_slots[EPI == EPI_ROPE_KV ? kRopeRows : 1];  // EPI_ROPE_KV: the rows' cache slots
+  // EPI_ROPE_KV: the rows' cache slots as looked up, then with the
+  // later-row-wins rule applied, and the rows' positions
+  __shared__ int rk_slots[EPI == EPI_ROPE_KV ? kRopeRows : 1];
+  __shared__ int rk_res[EPI == EPI_ROPE_KV ? kRopeRows : 1];
+  __shared__ int rk_pos[EPI == EPI_ROPE_KV ? kRopeRows : 1];
 
   // the activation block: column 16 mt + r (rows past M repeat row M - 1;
   // their results are dropped)
@@ -849,8 +870,8 @@ __global__ __launch_bounds__(1024) void gemv_xs_kernel(const GemvArgs args) {
       const int nb = t * 16 + 4 * kb;
       if (m < M && t < t_end) {
         if constexpr (EPI == EPI_ROPE_KV) {  // NMAT == 1; the pairs are (nb, nb+1), (nb+2, nb+3)
-          rope_kv_pair(args, rk_slots, m, nb, v[0][0], v[0][1]);
-          rope_kv_pair(args, rk_slots, m, nb + 2, v[0][2], v[0][3]);
+          rope_kv_pair<true>(args, rk_res, m, nb, v[0][0], v[0][1], rk_pos);
+          rope_kv_pair<true>(args, rk_res, m, nb + 2, v[0][2], v[0][3], rk_pos);
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -872,7 +893,8 @@ __global__ __launch_bounds__(1024) void gemv_xs_kernel(const GemvArgs args) {
   // loop refills the same registers in place every iteration, so no buffer
   // is copied across it.  The steps for a tile past the run compute on
   // re-read data and store nothing.
-  // EPI_ROPE_KV: the rows' cache slots, in LDS before the first barrier
+  // EPI_ROPE_KV: the rows' cache slots, in LDS before the first barrier,
+  // resolved after it (the loop's barrier precedes the first epilogue)
   if constexpr (EPI == EPI_ROPE_KV) rope_fill_slots(args, rk_slots);
 
   Buf b;
@@ -880,6 +902,7 @@ __global__ __launch_bounds__(1024) void gemv_xs_kernel(const GemvArgs args) {
   __builtin_amdgcn_sched_barrier(0);
   stage(b, 0);
   __syncthreads();
+  if constexpr (EPI == EPI_ROPE_KV) rope_resolve_slots(args, rk_slots, rk_res, rk_pos);
   int it = 0;
   for (int t = t_begin; t < t_end; ++t, ++it) {
     issue_sz(t + 1, b.sz);
