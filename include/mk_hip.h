@@ -256,7 +256,7 @@ int mk_quantize_kv(const void* src, uint8_t* codes, f16_storage_t* scales, int64
 
 /* Workspace (bytes, 16-byte aligned) the split-context attention kernels
  * need for B sequences of at most max_blocks pages, Hq query / Hkv key-value
- * heads of dimension D, on the current device.  Its first 64 KiB hold
+ * heads of dimension D, on the current device.  Its first 128 KiB hold
  * arrival counters: fill the workspace with zeros once, before its first
  * call; every call leaves the counters zero again, so the buffer can then be
  * reused without clearing (the rest holds split partials, any content).

@@ -1174,7 +1174,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 
 // ------------------------------------------------------- short-context plan
 // A small total context (B x blocks per block-table row x units at most
-// kSpMaxWaveBlocks) runs on a grid laid out from the block-table width
+// kSpMaxWaveBlocks, see sp_plan) runs on a grid laid out from the block-table width
 // instead of the lengths.  Sequence b's 32-position blocks are cut into splits
 // of sp_blk blocks, one wave per (split, unit), and sp_nw consecutive splits
 // of one (sequence, unit) share a workgroup.  So nothing on the way to the
@@ -1205,6 +1205,12 @@ __device__ __forceinline__ void store_agent(float* p, float v) {
 #define MK_ATTN_SP_WAVES 2048
 #endif
 constexpr int64_t kSpMaxWaveBlocks = MK_ATTN_SP_MAXWB;  // B x blocks x units on the short-context plan
+// ... or up to twice that when no table row exceeds kSpShortRowBlocks blocks
+// (4096 positions), so a sequence shorter than its row leaves few idle splits
+// (measured: 32 sequences of 2112 positions 53.4 -> 49.4 us per call; config 3,
+// rows of 256 blocks, stays on the stream plan)
+constexpr int64_t kSpMaxWaveBlocksShort = 2 * kSpMaxWaveBlocks;
+constexpr int64_t kSpShortRowBlocks = 128;
 constexpr int64_t kSpWaves = MK_ATTN_SP_WAVES;          // waves it aims for (one round on 256 CUs)
 constexpr int kSpMergeTrip = 16;                        // partials the final merge reads per trip
 
@@ -1608,8 +1614,9 @@ inline void split_plan(PagedArgs& a, int kvf) {
 }
 
 // Short-context plan (paged_attn_sp_kernel), taken when the block-table
-// width keeps B x blocks x units within kSpMaxWaveBlocks and pages hold a
-// multiple of 16 positions: blocks per split sized for about kSpWaves
+// width keeps B x blocks x units within kSpMaxWaveBlocks (twice that for rows
+// of at most kSpShortRowBlocks blocks) and pages hold a multiple of 16
+// positions: blocks per split sized for about kSpWaves
 // waves, then the widest workgroup (8, 4 or 2 splits) that still gives every
 // CU a workgroup, no wider than the splits of a sequence, and with its LDS
 // merge buffer within 64 KiB.
@@ -1621,7 +1628,7 @@ inline void sp_plan(PagedArgs& a, int64_t D) {
   if (a.P % 16 != 0) return;
   const int64_t blk = ((int64_t)a.MB * a.P + kBlockPos - 1) / kBlockPos;
   const int64_t wb = (int64_t)a.B * blk * a.units;
-  if (wb > kSpMaxWaveBlocks) return;
+  if (wb > kSpMaxWaveBlocks && !(wb <= kSpMaxWaveBlocksShort && blk <= kSpShortRowBlocks)) return;
   const int64_t c = (wb + kSpWaves - 1) / kSpWaves;
   if (c * kBlockPos / a.P + 1 > 64) return;  // a split's page ids must fit the 64 lanes
   const int64_t S = (blk + c - 1) / c;       // splits per sequence
@@ -1643,10 +1650,10 @@ inline int64_t workspace_slots(const PagedArgs& a) { return (int64_t)a.max_pairs
 
 // Workspace: [arrival counters, kCounterBytes][O partials fp32][(m, l) fp32].
 // The counters sit at the same place for every shape (the short-context
-// plan has at most kSpMaxWaveBlocks of them); the partials are
+// plan has at most kSpMaxWaveBlocksShort of them); the partials are
 // slots * Hq * (D + 2) floats for the stream plan and B * Hq * sp_nwg * (D + 2)
 // for the short-context plan.
-constexpr size_t kCounterBytes = (size_t)kSpMaxWaveBlocks * sizeof(int);
+constexpr size_t kCounterBytes = (size_t)kSpMaxWaveBlocksShort * sizeof(int);
 inline size_t workspace_need(const PagedArgs& a, int64_t D) {
   const int64_t stream_rows = workspace_slots(a) * a.Hq;
   const int64_t sp_rows = a.sp_nw ? (int64_t)a.B * a.Hq * a.sp_nwg : 0;

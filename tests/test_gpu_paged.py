@@ -77,9 +77,18 @@ def test_paged_update_collision_later_b_wins(dev):
 # ------------------------------------------------------------ fp16 paged attention
 
 # The short-context plan runs while B x 32-position blocks per table row x
-# units (kv heads x blocks of 16 query heads) is at most this; its arrival
-# counters (4 bytes each) lead the workspace.
+# units (kv heads x blocks of 16 query heads) is at most SP_MAX_WAVE_BLOCKS,
+# or twice that with rows of at most SP_SHORT_ROW_BLOCKS blocks; its arrival
+# counters (4 bytes each, 2 x SP_MAX_WAVE_BLOCKS of them) lead the workspace.
 SP_MAX_WAVE_BLOCKS = 16384
+SP_SHORT_ROW_BLOCKS = 128
+
+
+def _stream_width(B, units, P, mb):
+    """Pages per table row that put a call on the stream plan: rows longer
+    than SP_SHORT_ROW_BLOCKS blocks and B x blocks x units past
+    SP_MAX_WAVE_BLOCKS."""
+    return max(mb, -(-(SP_SHORT_ROW_BLOCKS + 1) * 32 // P), -(-(SP_MAX_WAVE_BLOCKS + 1) * 32 // (B * units * P)) + 1)
 
 
 def _pad_table(bt, NP, width, seed):
@@ -173,7 +182,7 @@ def test_paged_attention_short_context_split(dev, lengths, wide):
     B, Hq, Hkv, D, P = len(lengths), 32, 8, 128, 16
     mb = (max(lengths) + P - 1) // P
     q, Kp, Vp, bt, lengths = _case(31 + sum(lengths), B, Hq, Hkv, D, P, mb, lengths=lengths)
-    btw = _pad_table(bt, Kp.shape[0], max(mb, SP_MAX_WAVE_BLOCKS * 32 // (B * 8 * P) + 2), 10) if wide else bt
+    btw = _pad_table(bt, Kp.shape[0], _stream_width(B, 8, P, mb), 10) if wide else bt
     qt, Kt, Vt = (_t(a, dev, torch.float16) for a in (q, Kp, Vp))
     got = gqa.paged_gqa_decode_attention(qt[:, None], Kt, Vt, to_dev(btw, dev), to_dev(lengths, dev))[:, 0]
     ref = op.paged_attention(qt.float().cpu().numpy(), Kt.float().cpu().numpy(), Vt.float().cpu().numpy(), bt,
@@ -257,10 +266,10 @@ STREAM_CASES = [
 @pytest.mark.parametrize("B,Hq,Hkv,D,P,mb,lengths", STREAM_CASES)
 def test_paged_attention_stream_plan(dev, B, Hq, Hkv, D, P, mb, lengths):
     """Shapes the short-context plan would take, run on the stream plan through
-    a block table wide enough (B x 32-position blocks x units > SP_MAX_WAVE_BLOCKS)."""
+    a block table wide enough (_stream_width)."""
     q, Kp, Vp, bt, lengths = _case(200 + B + D, B, Hq, Hkv, D, P, mb, lengths=lengths)
     units = Hkv * ((Hq // Hkv + 15) // 16)
-    width = max(mb, -(-(SP_MAX_WAVE_BLOCKS + 1) * 32 // (B * units * P)) + 1)
+    width = _stream_width(B, units, P, mb)
     btw = _pad_table(bt, Kp.shape[0], width, 9)
     qt, Kt, Vt = (_t(a, dev, torch.float16) for a in (q, Kp, Vp))
     got = gqa.paged_gqa_decode_attention(qt[:, None], Kt, Vt, to_dev(btw, dev), to_dev(lengths, dev))[:, 0]
@@ -272,7 +281,7 @@ def test_paged_attention_stream_plan(dev, B, Hq, Hkv, D, P, mb, lengths):
 def _counters_zero(dev):
     from mk import _lib
     buf = _lib._WORKSPACES[(torch.device(dev).index, torch.cuda.current_stream(dev).cuda_stream)]
-    return bool(torch.all(buf[:4 * SP_MAX_WAVE_BLOCKS] == 0).item())
+    return bool(torch.all(buf[:8 * SP_MAX_WAVE_BLOCKS] == 0).item())
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -289,6 +298,7 @@ def test_paged_attention_short_plan_calls_in_a_row(dev, dtype):
         (3, 32, 8, 128, 16, 512, [4096, 8192, 31]),  # three blocks per split
         (2, 32, 8, 64, 32, 64, [2048, 1]),
         (16, 32, 8, 128, 16, 137, [2100 - 7 * i for i in range(16)]),  # five blocks per split
+        (32, 32, 8, 128, 16, 137, [2112 - 3 * i for i in range(32)]),  # short rows: the wider limit
         (1, 32, 8, 128, 16, 137, [2049]),
     ]
     for i, (B, Hq, Hkv, D, P, mb, lengths) in enumerate(cases):
