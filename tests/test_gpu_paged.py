@@ -312,6 +312,38 @@ def test_paged_attention_short_plan_calls_in_a_row(dev, dtype):
         assert _counters_zero(dev), f"arrival counters left non-zero after call {i}"
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_paged_attention_random_shapes(dev, seed):
+    """Seeded random geometries against the oracle, over both plans: batch,
+    GQA group (MHA .. MQA, one or two 16-head blocks), D 64 / 128, page size
+    16 / 32 / 64, fp16 / bf16, lengths from 0 to the table's end, and a table
+    sometimes much wider than the longest sequence."""
+    rng = np.random.default_rng(1000 + seed)
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    G = int(rng.choice([1, 2, 4, 8, 32]))
+    Hq, D, P = Hkv * G, int(rng.choice([64, 128])), int(rng.choice([16, 32, 64]))
+    B = int(rng.integers(1, 12))
+    mb = int(rng.integers(1, 2048 // P + 1))
+    lengths = rng.integers(0, mb * P + 1, size=B)
+    lengths[rng.integers(0, B)] = mb * P
+    if seed % 3 == 0:
+        lengths[rng.integers(0, B)] = 0
+    dtype = torch.float16 if seed % 2 == 0 else torch.bfloat16
+    q, Kp, Vp, bt, lengths = _case(2000 + seed, B, Hq, Hkv, D, P, mb, lengths=lengths)
+    units = Hkv * ((G + 15) // 16)
+    width = _stream_width(B, units, P, mb) if seed % 4 == 1 else mb
+    btw = _pad_table(bt, Kp.shape[0], width, 11) if width > mb else bt
+    qt, Kt, Vt = _t(q, dev, dtype), _t(Kp, dev, dtype), _t(Vp, dev, dtype)
+    print(f"random attention seed {seed}: B={B} Hq={Hq} Hkv={Hkv} D={D} P={P} mb={mb} width={width} {dtype}",
+          flush=True)
+    got = gqa.paged_gqa_decode_attention(qt[:, None], Kt, Vt, to_dev(btw, dev), to_dev(lengths, dev))[:, 0]
+    ref = op.paged_attention(qt.float().cpu().numpy(), Kt.float().cpu().numpy(), Vt.float().cpu().numpy(), bt,
+                             lengths)
+    tol = (1e-2, 1e-3) if dtype == torch.float16 else (3e-2, 4e-3)
+    assert_close(got, ref, rtol=tol[0], atol=tol[1], what=f"random seed {seed}")
+    assert torch.all(got[lengths == 0] == 0)
+
+
 def test_config3_full_size(dev):
     """B=16, 32/8 heads, D=128, P=16, lengths U[512,8192],
     permuted block table -- full size against the oracle."""
