@@ -112,6 +112,9 @@ TILE_CASES = [
     # uneven halves per wave and no zero points
     (8, 4096, 14336, 64, "sym"),
     (5, 1024, 2048, 32, "affine"),
+    # ... at 6 and 7 rows with uneven halves per wave (2 or 3; 1 or 2)
+    (6, 2048, 5120, 64, "none"),
+    (7, 1040, 3072, 64, "affine"),
     (20, 2048, 6272, 128, "none"),
     (17, 8192, 4096, 128, "none"),
     (33, 8192, 1024, 64, "sym"),
