@@ -85,6 +85,10 @@ class NativeLibraryError(RuntimeError):
     """The HIP library is missing or cannot be loaded."""
 
 
+# mk_abi_version() of the library these signatures describe
+ABI_VERSION = 1
+
+
 def library_path() -> Path:
     override = os.environ.get("MK_HIP_LIBRARY")
     return Path(override) if override else LIB_PATH
@@ -109,6 +113,11 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.argtypes = argtypes
             fn.restype = _RESTYPES.get(name, _I)
+        found = lib.mk_abi_version()
+        if found != ABI_VERSION:
+            raise NativeLibraryError(
+                f"{path} has ABI version {found}, this binding expects {ABI_VERSION}; rebuild the library"
+            )
         _lib = lib
         return lib
 

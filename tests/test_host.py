@@ -66,7 +66,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_workspace():
     lib = _lib.load()
-    assert lib.mk_abi_version() == 1
+    assert lib.mk_abi_version() == _lib.ABI_VERSION == 1
     # split-KV partials: B*Hq*splits*(D+2) fp32, never 0 for a real shape
     ws = _lib.workspace_bytes(16, 32, 8, 128, 512, 16)
     assert ws > 0 and ws % 4 == 0
@@ -329,3 +329,11 @@ def test_weight_quantizer_validation():
         qw.quantize_weight_groupwise(torch.zeros(4), qw.QuantizationConfig())
     with pytest.raises(ValueError, match="ROCm device"):
         qw.quantize_weight_groupwise(torch.zeros(2, 64), qw.QuantizationConfig())
+
+
+def test_loader_rejects_another_abi_version(monkeypatch):
+    """A library built for another ABI version fails at load, not at a call."""
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "ABI_VERSION", _lib.ABI_VERSION + 1)
+    with pytest.raises(_lib.NativeLibraryError, match="ABI version"):
+        _lib.load()
