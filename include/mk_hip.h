@@ -114,8 +114,8 @@ int mk_q8_gate_up(const void* x, const uint8_t* w_gate, const uint8_t* w_up,
 /* The front of quantized_mlp_block -- ops/mlp_block_ops.py:343-356: residual
  * add z = x + residual (z_out [M,K]), RMSNorm normed = z * rsqrt(mean(z^2) +
  * eps) * norm_w (normed_out [M,K]), then the gate/up products and SwiGLU as
- * mk_q4_gate_up / mk_q8_gate_up.  For q4 with an M = 1 fp16 row, K <= 8192,
- * fp16 norm weights and fp16 scales this is one launch (the norm runs inside
+ * mk_q4_gate_up / mk_q8_gate_up.  For q4 or q8 with an M = 1 fp16 row, K <=
+ * 8192, fp16 norm weights and fp16 scales this is one launch (the norm runs inside
  * the gate/up kernel) and normed_out may be NULL; otherwise the norm kernel
  * and the gate/up kernel run in turn through normed_out, which is then
  * required (MK_ERR_INVALID when NULL).

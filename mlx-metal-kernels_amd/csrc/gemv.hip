@@ -2001,7 +2001,7 @@ int norm_gate_up_entry(const void* x, const void* residual, const void* norm_w, 
   a.y2 = mlp_out;
   bool fast;
   gemv_prepare<BITS, 2>(a, N, K, gs, &fast);
-  if constexpr (BITS == 4) {
+  {
     // K <= 8192: the row fits two 16-byte chunks per thread of the workgroup
     if (nw_dt == MK_DT_F16 && K <= 4 * 2048 && M == 1 && dot_eligible<BITS, 2>(a, fast, M, act_dt, sc_dt) &&
         mk_aligned(residual, 16) &&

@@ -6,10 +6,10 @@ Composition (ops/mlp_block_ops.py:301-364):
 with every intermediate rounded to the activation dtype, as in the reference.
 
 When every stage runs on the HIP backend the block is two launches for a q4
-decode row (three otherwise) instead of six -- the rounding points are
-unchanged:
+or q8 fp16 decode row (three otherwise) instead of six -- the rounding points
+are unchanged:
     1. residual add + RMSNorm, gate + up matvec, SwiGLU epilogue
-       (mk_q{4,8}_rmsnorm_gate_up: one kernel for a q4 fp16 decode row, the
+       (mk_q{4,8}_rmsnorm_gate_up: one kernel for an fp16 decode row, the
        norm kernel then the gate/up kernel otherwise)
     2. down matvec, residual epilogue     (mk_q{4,8}_matvec with residual)
 """

@@ -291,7 +291,7 @@ def test_gate_up_and_swiglu_epilogue(dev, bits, rows, N, K, g):
                                             (8, 14336, 4096, 64, "f16"), (5, 8192, 2048, 32, "f16"),
                                             (16, 8192, 1024, 128, "f16")])
 def test_rmsnorm_gate_up(dev, bits, rows, N, K, g, act):
-    """mk_q{4,8}_rmsnorm_gate_up (one launch for a q4 fp16 row, the norm and
+    """mk_q{4,8}_rmsnorm_gate_up (one launch for an fp16 row, the norm and
     gate/up kernels otherwise) against the separate norm kernel and the oracle."""
     import mk.norm_ops as norm
 
