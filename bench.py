@@ -423,17 +423,26 @@ def cpu_baseline(sets, x_res_nw, budget_s=20.0):
 
 
 def cpu_model():
-    """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo)."""
+    """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo),
+    with its family / model / stepping: a hypervisor may shorten the name (to
+    "AMD EPYC", say), and those three numbers still name the core."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.lower().startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break  # the first processor's block is enough
+                key, _, val = line.partition(":")
+                fields[key.strip().lower()] = val.strip()
     except OSError:
         pass
-    import platform
+    name = fields.get("model name")
+    if not name:
+        import platform
 
-    return platform.processor() or "unknown"
+        return platform.processor() or "unknown"
+    ids = [f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields]
+    return f"{name} ({', '.join(ids)})" if ids else name
 
 
 def cpu_other_configs(budget_s=6.0):
