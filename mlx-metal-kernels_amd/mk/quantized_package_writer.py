@@ -1,31 +1,50 @@
-"""Writes a quantized package's payload -- one .npy file per array under
-``<output>/<tensor_subdir>/`` -- and then its ``package.json``
-(models/quantized_package_writer.py).
+"""Writer of a quantized package's payload and ``package.json``.
 
-File names follow the reference: ``layers.<i>.<key>.weight.npy`` /
-``.scales.npy`` / ``.zeros.npy`` for the projections,
-``layers.<i>.<norm key>.weight.npy`` for the norms and
-``<name>.weight.npy`` for global tensors.  The metadata records each
-relative path and the SHA-256 of the data (weight) file; ``package.json`` is
-written only when every tensor was written.  Arrays may be numpy arrays or
-torch tensors (device tensors are copied to the host).
+What is fixed by the on-disk format (models/quantized_package_writer.py:42-206,
+the files and fields the reference's loader and ours read back):
+
+* one ``.npy`` per array under ``<output>/<tensor_subdir>/``, named
+  ``layers.<i>.<key>.weight.npy`` / ``.scales.npy`` / ``.zeros.npy`` for a
+  projection, ``layers.<i>.<norm key>.weight.npy`` for a norm (taken from the
+  layer package's ``<key>_weight`` attribute) and ``<name>.weight.npy`` for a
+  global tensor;
+* the metadata records those names relative to the tensor folder and the
+  SHA-256 of each weight (data) file;
+* ``package.json`` is written only when every tensor was written; the report
+  carries the same fields, messages and counts.
+
+How it is done here: the writer first turns the metadata into a flat plan --
+one entry per tensor, holding the files to write and where each name goes in
+the metadata -- without touching the disk (a dry run is that plan's size).  It
+then streams every array through a sink that feeds the file and the hash
+together, so each payload is written once and never read back to checksum
+it, and records a tensor's file names and checksum in the metadata only once
+all of that tensor's files are on disk.  Arrays may be numpy arrays or torch
+tensors (device tensors are copied to the host).
 """
 
 from __future__ import annotations
 
+import hashlib
 from dataclasses import dataclass, field
 from pathlib import Path
 from typing import Any
 
+import numpy as np
+
 from .quantized_layer_package import QuantizedLlamaLayerPackage
 from .quantized_package_io import QuantizedCheckpointPackage, QuantizedTensorMetadata
-from .tensor_data_io import save_tensor_npy
+from .tensor_data_io import _as_numpy
+
+_CHECKSUMS = ("sha256", "sha1", "md5")
+_NORM_ROLES = ("norm", "final_norm")
 
 
 @dataclass
 class PackageWriterConfig:
     """models/quantized_package_writer.py:12-24.  ``checksum_algorithm`` is
-    validated but, as in the reference, the recorded checksums are SHA-256."""
+    validated, but the recorded checksums are SHA-256, the digest the
+    package loader verifies."""
 
     tensor_subdir: str = "tensors"
     checksum_algorithm: str = "sha256"
@@ -33,8 +52,9 @@ class PackageWriterConfig:
     def validate(self) -> "PackageWriterConfig":
         if not self.tensor_subdir:
             raise ValueError("tensor_subdir must be non-empty")
-        if self.checksum_algorithm not in ("sha256", "sha1", "md5"):
-            raise ValueError(f"checksum_algorithm must be one of sha256, sha1, md5, got {self.checksum_algorithm!r}")
+        if self.checksum_algorithm not in _CHECKSUMS:
+            raise ValueError(f"checksum_algorithm must be one of {', '.join(_CHECKSUMS)}, "
+                             f"got {self.checksum_algorithm!r}")
         return self
 
 
@@ -57,12 +77,83 @@ class PackageWriterReport:
 
 @dataclass
 class TensorWriteInfo:
+    """One written tensor: its data file and the data's size in bytes."""
+
     file_path: str
     nbytes: int
 
 
+class _HashSink:
+    """File-like target for ``np.lib.format.write_array``: every piece goes to
+    the file and into the digest, so the checksum needs no second read."""
+
+    def __init__(self, fh, digest):
+        self._fh = fh
+        self._digest = digest
+
+    def write(self, data) -> int:
+        self._digest.update(data)
+        return self._fh.write(data)
+
+
+def _stream_npy(array: Any, path: Path) -> tuple[int, str]:
+    """Write ``array`` as numpy's ``.npy`` encoding (the bytes ``np.save``
+    produces) and return (data bytes, SHA-256 of the file)."""
+    arr = _as_numpy(array)
+    if arr.dtype.hasobject:
+        raise TypeError("object arrays cannot be written to a tensor payload")
+    path.parent.mkdir(parents=True, exist_ok=True)
+    digest = hashlib.sha256()
+    with path.open("wb") as fh:
+        np.lib.format.write_array(_HashSink(fh, digest), arr, allow_pickle=False)
+    return int(arr.nbytes), digest.hexdigest()
+
+
+# (metadata field, file suffix); the first file of a tensor is its data file
+_PROJ_FILES = (("data_file", ".weight.npy"), ("scales_file", ".scales.npy"), ("zeros_file", ".zeros.npy"))
+_WEIGHT_ONLY = (("data_file", ".weight.npy"),)
+
+
+@dataclass
+class _Entry:
+    """One tensor of the plan: the error label, the files as (metadata
+    field, relative name, array), the metadata object to fill in, or the
+    reason the tensor cannot be written."""
+
+    label: str
+    files: list[tuple[str, str, Any]] = field(default_factory=list)
+    meta: QuantizedTensorMetadata | None = None
+    problem: str | None = None
+
+
+def _layer_entry(layer_idx: int, key: str, meta: QuantizedTensorMetadata,
+                 pkg: QuantizedLlamaLayerPackage) -> _Entry:
+    entry = _Entry(label=f"layer {layer_idx}, tensor {key}", meta=meta)
+    stem = f"layers.{layer_idx}.{key}"
+    if meta.role in _NORM_ROLES:
+        attr = key if key.endswith("_weight") else f"{key}_weight"
+        weight = getattr(pkg, attr, None)
+        if weight is None:
+            entry.problem = f"layer {layer_idx}: no weight attribute for norm {key}"
+            return entry
+        arrays: tuple[Any, ...] = (weight,)
+        spec = _WEIGHT_ONLY
+    else:
+        lin = getattr(pkg, key, None)
+        if lin is None:
+            entry.problem = f"layer {layer_idx}: no attribute {key} on QuantizedLlamaLayerPackage"
+            return entry
+        arrays = (lin.weight, lin.scales, lin.zeros)
+        spec = _PROJ_FILES
+    for (slot, suffix), arr in zip(spec, arrays):
+        if arr is not None:
+            entry.files.append((slot, stem + suffix, arr))
+    return entry
+
+
 class QuantizedPackageWriter:
-    """models/quantized_package_writer.py:42-206."""
+    """models/quantized_package_writer.py:42-206 (the files, metadata fields
+    and report it produces)."""
 
     def __init__(self, config: PackageWriterConfig | None = None):
         self._config = (config or PackageWriterConfig()).validate()
@@ -70,86 +161,69 @@ class QuantizedPackageWriter:
     def config(self) -> PackageWriterConfig:
         return self._config
 
-    @staticmethod
-    def _tensor_rel_path(layer_idx: int | None, name: str, suffix: str) -> str:
-        return f"layers.{layer_idx}.{name}{suffix}" if layer_idx is not None else f"{name}{suffix}"
+    # -- plan --------------------------------------------------------------
+    def plan(self, package: QuantizedCheckpointPackage, layer_packages: list[QuantizedLlamaLayerPackage],
+             global_tensors: dict[str, Any] | None = None) -> list[_Entry]:
+        """The tensors a write would produce, in write order, with no I/O.  A
+        layer without a package is one entry that cannot be written."""
+        found = {p.layer_idx: p for p in layer_packages}
+        entries: list[_Entry] = []
+        for layer in package.layers:
+            pkg = found.get(layer.layer_idx)
+            if pkg is None:
+                entries.append(_Entry(label=f"layer {layer.layer_idx}", problem="no QuantizedLlamaLayerPackage provided"))
+                continue
+            entries.extend(_layer_entry(layer.layer_idx, key, meta, pkg) for key, meta in layer.tensors.items())
+        for name, data in (global_tensors or {}).items():
+            entries.append(_Entry(label=f"global tensor {name}", files=[("data_file", f"{name}.weight.npy", data)],
+                                  meta=package.global_tensors.get(name)))
+        return entries
+
+    # -- execute -----------------------------------------------------------
+    def _write_entry(self, tdir: Path, entry: _Entry) -> TensorWriteInfo:
+        if entry.problem is not None:
+            raise ValueError(entry.problem)
+        written: list[tuple[str, str, int, str]] = []
+        for slot, rel, arr in entry.files:
+            nbytes, digest = _stream_npy(arr, tdir / rel)
+            written.append((slot, rel, nbytes, digest))
+        _, data_rel, data_bytes, data_digest = written[0]
+        if entry.meta is not None:  # recorded only once every file is on disk
+            for slot, rel, _, _ in written:
+                setattr(entry.meta, slot, rel)
+            entry.meta.checksum = data_digest
+        return TensorWriteInfo(file_path=str(tdir / data_rel), nbytes=data_bytes)
 
     def write_tensors(self, package: QuantizedCheckpointPackage, layer_packages: list[QuantizedLlamaLayerPackage],
                       output_dir: str | Path, *, global_tensors: dict[str, Any] | None = None) -> PackageWriterReport:
-        """Write every layer tensor the metadata lists (from the matching layer
-        package) and every global tensor given, filling in the metadata's file
-        names and checksums; errors are collected per tensor, not raised."""
+        """Write every planned tensor, fill in the metadata's file names and
+        checksums, and save ``package.json`` if nothing failed.  Failures are
+        reported per tensor, not raised."""
         out = Path(output_dir)
         tdir = out / self._config.tensor_subdir
-        files, errors = [], []
-        total = count = 0
-        by_idx = {p.layer_idx: p for p in layer_packages}
-        for meta in package.layers:
-            pkg = by_idx.get(meta.layer_idx)
-            if pkg is None:
-                errors.append(f"layer {meta.layer_idx}: no QuantizedLlamaLayerPackage provided")
-                continue
-            for key, tmeta in meta.tensors.items():
-                try:
-                    info = self._write_layer_tensor(tdir, meta.layer_idx, key, tmeta, pkg)
-                    files.append(info.file_path)
-                    total += info.nbytes
-                    count += 1
-                except Exception as exc:  # noqa: BLE001 - reported per tensor
-                    errors.append(f"layer {meta.layer_idx}, tensor {key}: {exc}")
-        for name, data in (global_tensors or {}).items():
+        report = PackageWriterReport(ok=False)
+        for entry in self.plan(package, layer_packages, global_tensors):
             try:
-                tmeta = package.global_tensors.get(name)
-                rel = self._tensor_rel_path(None, name, ".weight.npy")
-                info = save_tensor_npy(data, tdir / rel)
-                if tmeta:
-                    tmeta.data_file = rel
-                    tmeta.checksum = info.checksum
-                files.append(info.file_path)
-                total += info.nbytes
-                count += 1
-            except Exception as exc:  # noqa: BLE001
-                errors.append(f"global tensor {name}: {exc}")
-        path = str(out / "package.json")
-        if not errors:
-            package.save_json(out / "package.json")
-        return PackageWriterReport(ok=not errors, files_written=files, errors=errors, warnings=[], tensor_count=count,
-                                   total_bytes=total, package_path=path if (not errors or files) else None)
-
-    def _write_layer_tensor(self, tdir: Path, layer_idx: int, key: str, tmeta: QuantizedTensorMetadata,
-                            pkg: QuantizedLlamaLayerPackage) -> TensorWriteInfo:
-        if tmeta.role in ("norm", "final_norm"):
-            attr = key if key.endswith("_weight") else f"{key}_weight"
-            weight = getattr(pkg, attr, None)
-            if weight is None:
-                raise ValueError(f"layer {layer_idx}: no weight attribute for norm {key}")
-            rel = self._tensor_rel_path(layer_idx, key, ".weight.npy")
-            info = save_tensor_npy(weight, tdir / rel)
-            tmeta.data_file = rel
-            tmeta.checksum = info.checksum
-            return TensorWriteInfo(file_path=info.file_path, nbytes=info.nbytes)
-        lin = getattr(pkg, key, None)
-        if lin is None:
-            raise ValueError(f"layer {layer_idx}: no attribute {key} on QuantizedLlamaLayerPackage")
-        rel_w = self._tensor_rel_path(layer_idx, key, ".weight.npy")
-        rel_s = self._tensor_rel_path(layer_idx, key, ".scales.npy")
-        winfo = save_tensor_npy(lin.weight, tdir / rel_w)
-        save_tensor_npy(lin.scales, tdir / rel_s)
-        tmeta.data_file = rel_w
-        tmeta.scales_file = rel_s
-        tmeta.checksum = winfo.checksum
-        if lin.zeros is not None:
-            rel_z = self._tensor_rel_path(layer_idx, key, ".zeros.npy")
-            save_tensor_npy(lin.zeros, tdir / rel_z)
-            tmeta.zeros_file = rel_z
-        return TensorWriteInfo(file_path=winfo.file_path, nbytes=winfo.nbytes)
+                info = self._write_entry(tdir, entry)
+            except Exception as exc:  # noqa: BLE001 - reported per tensor
+                report.errors.append(f"{entry.label}: {exc}")
+                continue
+            report.files_written.append(info.file_path)
+            report.total_bytes += info.nbytes
+            report.tensor_count += 1
+        json_path = out / "package.json"
+        report.ok = not report.errors
+        if report.ok:
+            package.save_json(json_path)
+        report.package_path = str(json_path) if (report.ok or report.files_written) else None
+        return report
 
     def write_package(self, package: QuantizedCheckpointPackage, layer_packages: list[QuantizedLlamaLayerPackage],
                       output_dir: str | Path, *, global_tensors: dict[str, Any] | None = None,
                       dry_run: bool = False) -> PackageWriterReport:
-        """write_tensors, or with ``dry_run`` only the count of tensors it would
-        write (nothing touches the disk)."""
+        """``write_tensors``; with ``dry_run`` only the number of tensors the
+        metadata and ``global_tensors`` name (nothing touches the disk)."""
         if dry_run:
-            n = sum(len(l.tensors) for l in package.layers) + len(global_tensors or {})
-            return PackageWriterReport(ok=True, tensor_count=n, package_path=str(Path(output_dir) / "package.json"))
+            count = sum(len(layer.tensors) for layer in package.layers) + len(global_tensors or {})
+            return PackageWriterReport(ok=True, tensor_count=count, package_path=str(Path(output_dir) / "package.json"))
         return self.write_tensors(package, layer_packages, output_dir, global_tensors=global_tensors)
