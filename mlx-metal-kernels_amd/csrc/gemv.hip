@@ -26,6 +26,7 @@
 // The MFMA contraction is order-free in k, so the activation operand is built
 // in the same permuted k order the magic unpack produces.
 #include "common.h"
+#include "norm_chunks.h"
 #include "paged_common.h"
 
 namespace {
@@ -1272,24 +1273,31 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     issue_sz();
     __builtin_amdgcn_sched_barrier(0);  // keep the small loads ahead of the rest
   }
+  // residual epilogue: the lane that stores output (m, n0 + rr) requests its
+  // residual value now, with the operands, not after the reduction (which
+  // would add a memory trip to the last workgroup's tail); every lane loads
+  // (an in-range element where it stores nothing) so the load counts in order
+  f16 res_pre = (f16)0.0f;
+  if constexpr (EPI == EPI_RESIDUAL) {
+    const int m = lane / R, rr = lane - (lane / R) * R;
+    const bool st = lane < R * MR && n0 + rr < N && m < args.M;
+    res_pre = reinterpret_cast<const f16*>(args.residual)[st ? (size_t)m * N + n0 + rr : 0];
+  }
 
   // activations: NORM -- 16-byte chunks c = threadIdx.x (+ blockDim.x) of x,
   // the residual and the norm weight, at most two per thread (the dispatcher
   // keeps K / 8 <= 2 * blockDim.x), clamped so every load issues; otherwise
   // -- this lane's four vectors of its unit of x.
   const int nthr = blockDim.x;
-  const int nchunk = K / 8;
-  const bool two = nthr < nchunk;  // workgroup-uniform
   u32x4 ax[NORM ? 2 : 1], ar[NORM ? 2 : 1], aw[NORM ? 2 : 1];
   DotFrag<BITS, NMAT, R, MR> f;
   const int u = ubase + lane;
   const int k0 = (u < U ? u : 0) * 32;
   if constexpr (NORM) {
     // chunks past the row (threads beyond K / 8, which the norm below
-    // leaves out) re-read chunk 0, so every load stays inside the row
-    const int c0 = threadIdx.x, c1 = two ? threadIdx.x + nthr : threadIdx.x;
-    const int c0c = c0 < nchunk ? c0 : 0;
-    const int c1c = c1 < nchunk ? c1 : c0c;
+    // leaves out) re-read a chunk inside it, so every load stays in the row
+    const NormChunks nc = norm_prologue_chunks(threadIdx.x, nthr, K);
+    const int c0c = nc.c0, c1c = nc.c1;
     // no residual: the loads read x again and are dropped, so every load
     // still issues in order
     const f16* rp = reinterpret_cast<const f16*>(args.nres ? args.nres : args.x);
@@ -1300,7 +1308,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     ar[1] = ldg128(rp + 8 * c1c);
     aw[0] = ldg128(wp + 8 * c0c);
     aw[1] = ldg128(wp + 8 * c1c);
-    if (!args.nres) ar[0] = ar[1] = (u32x4){0u, 0u, 0u, 0u};
     __builtin_amdgcn_sched_barrier(0);
     issue_sz();
   } else {
@@ -1325,12 +1332,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
 
   if constexpr (NORM) {
     const int c0 = threadIdx.x, c1 = threadIdx.x + nthr;
-    const bool has0 = c0 < nchunk, has1 = two && c1 < nchunk;
+    const NormChunks nc = norm_prologue_chunks(threadIdx.x, nthr, K);
+    const bool has0 = nc.has0, has1 = nc.has1;
     {
       // z = fp16(x + r) and the row's sum of z^2 (the packed fp16 add rounds
       // the exact sum once, as the norm kernel's fp32 add-then-round does for
       // fp16 inputs), then n = fp16((z * inv) * w) in fp32 -- the arithmetic
-      // of rms_norm_vec_kernel; workgroup 0 writes z and n out
+      // of rms_norm_vec_kernel; workgroup 0 writes z and n out.  (No
+      // residual: the loads above read x again; they are dropped here, after
+      // the code requests, since selecting them waits for them.)
+      if (!args.nres) ar[0] = ar[1] = (u32x4){0u, 0u, 0u, 0u};
       u32x4 zz[2];
       float ss = 0.0f;
 #pragma unroll
@@ -1508,7 +1519,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     rope_kv_store(args, rk_slots, m, nn, v0);  // lane pairs (rr even, rr + 1) never straddle a head: R and D even
     return;
   }
-  if (nn < N && m < args.M) store_out<f16, EPI>(args, (size_t)m * N + nn, v0, v1);
+  if (nn < N && m < args.M) {
+    if constexpr (EPI == EPI_RESIDUAL) {  // store_out's arithmetic with the prefetched residual
+      const f16 d = saturate_cast<f16>(v0);
+      if (args.y0) reinterpret_cast<f16*>(args.y0)[(size_t)m * N + nn] = d;
+      reinterpret_cast<f16*>(args.y1)[(size_t)m * N + nn] = from_f32<f16>(to_f32(res_pre) + to_f32(d));
+    } else {
+      store_out<f16, EPI>(args, (size_t)m * N + nn, v0, v1);
+    }
+  }
 }
 
 // --------------------------------------------------------------------------
@@ -1735,6 +1754,7 @@ int launch_dot(GemvArgs a, hipStream_t st) {
   const size_t stage_bytes = (size_t)a.kw * a.rg * NMAT * R * 2 * (2 * SEG_STRIDE);
   const size_t lds = (NORM ? (size_t)a.K * 2 : 0) + stage_bytes;
   if constexpr (NORM) {
+    MK_REQUIRE(a.K / 8 <= 2 * (int)block.x);  // the prologue's two 16-byte chunks per thread cover the row
     gemv_dot_kernel<BITS, NMAT, EPI, true, 1><<<grid, block, lds, st>>>(a);
   } else {
     if (a.M <= 1) gemv_dot_kernel<BITS, NMAT, EPI, false, 1><<<grid, block, lds, st>>>(a);
