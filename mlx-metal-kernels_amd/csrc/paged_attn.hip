@@ -1194,6 +1194,22 @@ __device__ __forceinline__ void store_agent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Ordering of the partials before the arrival count.  By default the
+// count is a relaxed fetch_add after s_waitcnt vmcnt(0): under the HIP/C++
+// memory model the partial stores and the last workgroup's reads then race,
+// and the merge is correct only because of how this toolchain (ROCm 7.x
+// clang) lowers agent-scope relaxed stores on gfx950: write-through to
+// memory (sc1), complete once vmcnt reaches zero, so the last workgroup's
+// acquire (L1/L2 invalidate) sees them.  A compiler or ISA that lowered them
+// otherwise would break the merge silently and leave counters non-zero.
+// Building with -DMK_SP_MERGE_RELEASE=1 (make MKDEFS=-DMK_SP_MERGE_RELEASE=1)
+// makes the count a release fetch_add, which the memory model guarantees,
+// at the cost of an L2 write-back per workgroup; run the split-plan parity
+// tests under both builds when the toolchain changes.
+#ifndef MK_SP_MERGE_RELEASE
+#define MK_SP_MERGE_RELEASE 0
+#endif
+
 // Experiments: a fixed number of waves per workgroup (0: the plan's rule).
 #ifndef MK_ATTN_SP_NW
 #define MK_ATTN_SP_NW 0
@@ -1388,7 +1404,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   lds_barrier();
   if (threadIdx.x == 0) {
     int* ctr = a.cnt + (size_t)b * a.units + unit;
-    const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int prev = __hip_atomic_fetch_add(ctr, 1, MK_SP_MERGE_RELEASE ? __ATOMIC_RELEASE : __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
     const int last = prev == nwg - 1;
     if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     is_last = last;
