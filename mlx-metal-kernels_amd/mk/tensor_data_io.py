@@ -157,6 +157,10 @@ def load_tensor_to_device(file_path: str | Path, device, *, dtype=None, expected
         staging = [torch.empty(step, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
         done = [None, None]
         stream = torch.cuda.Stream(device=dev)
+        # `out` came from the current stream's pool: work still queued there
+        # may use its block (e.g. the previous call's dtype conversion read
+        # the tensor that block held), so the copies wait for that stream
+        stream.wait_stream(torch.cuda.current_stream(dev))
         for i, lo in enumerate(range(0, nbytes, step)):
             hi = min(lo + step, nbytes)
             buf = staging[i % 2]

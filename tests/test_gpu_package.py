@@ -36,6 +36,26 @@ def test_chunked_device_load_bit_exact(dev, tmp_path, shape, dtype, chunk):
     assert np.array_equal(got.cpu().numpy().view(np.uint8), arr.view(np.uint8))
 
 
+def test_device_load_with_conversion_in_a_row(dev, tmp_path):
+    """fp32 scales / zeros loaded with dtype=float16, several in a row behind
+    queued work on the current stream: each load's staging copies wait for
+    that stream, so the block freed by the previous call's conversion is not
+    overwritten while the conversion still reads it -- every result equals
+    numpy's fp16 rounding, bit for bit."""
+    print("fp32 -> fp16 loads in a row", flush=True)
+    rng = np.random.default_rng(7)
+    arrays = [rng.standard_normal((1024, 256)).astype(np.float32) for _ in range(6)]
+    infos = [tdio.save_tensor_npy(a, tmp_path / f"s{i}.npy") for i, a in enumerate(arrays)]
+    got = []
+    for info in infos:
+        torch.cuda._sleep(2_000_000)  # keep work queued on the current stream
+        got.append(tdio.load_tensor_to_device(info.file_path, dev, dtype=torch.float16, chunk_bytes=256 << 10))
+    torch.cuda.synchronize()
+    for a, t in zip(arrays, got):
+        assert t.dtype == torch.float16
+        assert np.array_equal(t.cpu().numpy().view(np.uint16), a.astype(np.float16).view(np.uint16))
+
+
 def _np_linear(rng, n, k, g):
     codes = rng.integers(0, 16, size=(n, k // 2), dtype=np.uint8) | (rng.integers(0, 16, size=(n, k // 2),
                                                                                    dtype=np.uint8) << 4)
