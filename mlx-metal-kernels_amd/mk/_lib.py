@@ -188,15 +188,39 @@ def workspace_bytes(B: int, Hq: int, Hkv: int, D: int, max_blocks: int, page_siz
     return int(load().mk_paged_attention_workspace_bytes(B, Hq, Hkv, D, max_blocks, page_size))
 
 
-# Zero-filled paged-attention workspaces, one per (device, stream).  The
-# library keeps arrival counters at the start of the workspace: they must be
+# Zero-filled workspaces, one per (kind, device, stream).  The library keeps
+# the attention's arrival counters at the start of a workspace: they must be
 # zero before a call and every call leaves them zero, so one buffer serves
 # every call issued on its stream (calls on one stream never overlap).
-# A graph captured on a stream keeps using the buffer that stream had at
-# capture time, so a replaced buffer is retired (kept alive), never freed.
+# A graph captured on a stream keeps using the buffer handed out during the
+# capture: such a buffer, once replaced by a larger one, is retired (kept
+# alive) rather than freed; any other replaced buffer is freed.  Graphs that
+# captured on the same stream share its buffer, so they must be replayed on
+# one stream, one after another (the decode graphs and bench.py do this).
 _WORKSPACES: dict = {}
 _RETIRED: list = []
+_CAPTURED: set = set()
 _WS_LOCK = threading.Lock()
+
+
+def _stream_workspace(kind: str, device: torch.device, nbytes: int):
+    size = (nbytes + 255) // 256 * 256
+    dev = torch.device(device)
+    key = (kind, dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    capturing = torch.cuda.is_current_stream_capturing()
+    with _WS_LOCK:
+        buf = _WORKSPACES.get(key)
+        if buf is None or buf.numel() < size:
+            old = buf
+            buf = torch.zeros(size, dtype=torch.uint8, device=dev)
+            if capturing:  # made inside the capture: the graph zero-fills it on every replay
+                return buf
+            if old is not None and old.data_ptr() in _CAPTURED:
+                _RETIRED.append(old)
+            _WORKSPACES[key] = buf
+        if capturing:
+            _CAPTURED.add(buf.data_ptr())
+    return buf
 
 
 def attention_workspace(device: torch.device, B: int, Hq: int, Hkv: int, D: int, max_blocks: int,
@@ -209,17 +233,5 @@ def attention_workspace(device: torch.device, B: int, Hq: int, Hkv: int, D: int,
     nbytes = workspace_bytes(B, Hq, Hkv, D, max_blocks, page_size)
     if nbytes <= 0:
         return None, 0
-    size = (nbytes + 15) // 16 * 16
-    dev = torch.device(device)
-    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
-    with _WS_LOCK:
-        buf = _WORKSPACES.get(key)
-        if buf is not None and buf.numel() >= size:
-            return buf, nbytes
-        old = buf
-        buf = torch.zeros(size, dtype=torch.uint8, device=dev)
-        if not torch.cuda.is_current_stream_capturing():
-            if old is not None:
-                _RETIRED.append(old)
-            _WORKSPACES[key] = buf
-    return buf, nbytes
+    return _stream_workspace("attention", device, nbytes), nbytes
+

@@ -280,7 +280,7 @@ def test_paged_attention_stream_plan(dev, B, Hq, Hkv, D, P, mb, lengths):
 
 def _counters_zero(dev):
     from mk import _lib
-    buf = _lib._WORKSPACES[(torch.device(dev).index, torch.cuda.current_stream(dev).cuda_stream)]
+    buf = _lib._WORKSPACES[("attention", torch.device(dev).index, torch.cuda.current_stream(dev).cuda_stream)]
     return bool(torch.all(buf[:8 * SP_MAX_WAVE_BLOCKS] == 0).item())
 
 
