@@ -90,6 +90,21 @@ def q8_matvec(x, q, scales, zeros=None, group_size=32, act="f16"):
     return matvec(x, _deq_act(np.asarray(q, dtype=np.uint8), scales, zeros, group_size, act), act)
 
 
+def q4_matvec_w32(x, packed, scales, zeros=None, group_size=32, act="f16"):
+    """The reference's Metal matvec backends (ops/quant_ops.py:529-571 running
+    kernels/q4_matvec_decode.metal:17-28): w = (q - z) s kept in fp32, fp32
+    accumulation, one rounding of each sum into x's dtype (clipped to its
+    finite range, as the HIP kernels saturate).  It differs from q4_matvec,
+    the pure-array reference, only by that path's fp16 rounding of W."""
+    K = x.shape[1]
+    return matvec(x, dequant(unpack_q4(packed, K), scales, zeros, group_size, np.float32), act)
+
+
+def q8_matvec_w32(x, q, scales, zeros=None, group_size=32, act="f16"):
+    """kernels/q8_matvec_decode.metal: the q8 twin of q4_matvec_w32."""
+    return matvec(x, dequant(np.asarray(q, dtype=np.uint8), scales, zeros, group_size, np.float32), act)
+
+
 def swiglu(gate: np.ndarray, up: np.ndarray, act: str = "f16") -> np.ndarray:
     """ops/activation_ops.py:83-88: g / (1 + exp(-g)) * u in fp32."""
     g = gate.astype(np.float32)
@@ -108,16 +123,23 @@ def rms_norm(x: np.ndarray, w: np.ndarray, eps: float = 1e-5) -> np.ndarray:
     return (xf * inv * w.astype(np.float32)).astype(x.dtype)
 
 
-def mlp_block(x, residual, norm_w, gate, up, down, bits=4, group_size=32, eps=1e-5, intermediates=False):
-    """ops/mlp_block_ops.py:258-364 (reference preset): gate/up/down are
-    (codes, scales, zeros) triples; x, residual [rows, D] fp16."""
-    mv = q4_matvec if bits == 4 else q8_matvec
+def mlp_block(x, residual, norm_w, gate, up, down, bits=4, group_size=32, eps=1e-5, intermediates=False,
+              w32=False):
+    """ops/mlp_block_ops.py:258-364: gate/up/down are (codes, scales, zeros)
+    triples; x, residual [rows, D] fp16.  w32=False is the reference preset
+    (:258-298, the pure-array matvecs, W rounded to fp16); w32=True the Metal
+    presets (:301-364 with matvec backends metal_*), whose kernels keep W in
+    fp32 (q4_matvec_w32 / q8_matvec_w32).  A pair (gate_up, down) picks the
+    semantics per projection."""
+    w32_gu, w32_dn = (w32, w32) if isinstance(w32, bool) else w32
+    pick = lambda exact: ((q4_matvec_w32 if bits == 4 else q8_matvec_w32) if exact
+                          else (q4_matvec if bits == 4 else q8_matvec))
     z = residual_add(x, residual)
     n = rms_norm(z, norm_w, eps)
-    g = mv(n, *gate, group_size=group_size)
-    u = mv(n, *up, group_size=group_size)
+    g = pick(w32_gu)(n, *gate, group_size=group_size)
+    u = pick(w32_gu)(n, *up, group_size=group_size)
     m = swiglu(g, u)
-    d = mv(m, *down, group_size=group_size)
+    d = pick(w32_dn)(m, *down, group_size=group_size)
     out = residual_add(z, d)
     if intermediates:
         return out, {"z": z, "normed": n, "gate": g, "up": u, "mlp": m, "down": d}

@@ -167,3 +167,31 @@ def test_full_shape_stack_step_with_llama3_head(dev, B):
         if got[b] != want[b]:
             lg = ref_logits[b]
             assert abs(lg[got[b]] - lg[want[b]]) <= 1e-2 * abs(lg[want[b]]) + e2e_atol * rms, (b, got[b], want[b])
+
+
+@pytest.mark.parametrize("B", [32, 17])
+def test_head_full_shape_batched(dev, B):
+    """The stack's final RMSNorm + 128256 x 4096 q4 head at decode batch 32
+    (config 5's benched batch: the norm kernel, then the activation-stationary
+    batched matvec over all 8016 row tiles) and at an odd batch: the whole
+    head runs on the device; the oracle checks the normalised rows and a
+    sample of 2,240 head rows -- the first and last 512 and every 97th between
+    them -- on the HIP normalised rows, at the kernel tolerance."""
+    rng = np.random.default_rng(800 + B)
+    print(f"full-shape head B={B}", flush=True)
+    hidden = rng.standard_normal((B, H)).astype(np.float16)
+    fnorm = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float16)
+    hc, hs, hz = _q4(rng, VOCAB, H)
+    from mk.quant_ops import q_rmsnorm_matvec
+    y, normed = q_rmsnorm_matvec(torch.from_numpy(hidden).to(dev), torch.from_numpy(fnorm).to(dev),
+                                 torch.from_numpy(hc).to(dev), torch.from_numpy(hs).to(torch.float16).to(dev),
+                                 torch.from_numpy(hz).to(torch.float16).to(dev), bits=4, group_size=G, eps=1e-5,
+                                 return_normed=True)
+    assert tuple(y.shape) == (B, VOCAB)
+    nrm = normed.cpu().numpy()
+    ref_n = oq.rms_norm(hidden, fnorm)
+    assert np.all(np.abs(nrm.astype(np.float32) - ref_n.astype(np.float32)) <= _ulp16(ref_n) + 1e-7)
+    rows = np.unique(np.concatenate([np.arange(512), np.arange(VOCAB - 512, VOCAB), np.arange(512, VOCAB - 512, 97)]))
+    got = y.float().cpu().numpy()[:, rows]
+    ref = oq.q4_matvec(nrm, hc[rows], hs[rows], hz[rows], group_size=G)
+    assert_close(got, ref, what=f"head rows B={B}")

@@ -131,6 +131,23 @@ def test_rms_norm_constant_row():
     assert np.allclose(y, 2.0 * 3.0 / math.sqrt(9.0 + 1e-5), rtol=1e-3)
 
 
+def test_rms_norm_eps_dominates_small_rows():
+    """Rows of amplitude ~1e-3, where eps (1e-5, ops/norm_ops.py:47) is ten
+    times mean(x^2): a constant row c gives c / sqrt(c^2 + eps) -- 0.30151
+    for c = 1e-3 (without eps it would be 1.0, with eps 1e-6 0.7071) -- and
+    the default eps is the reference's.  An all-zero row stays zero."""
+    x = np.full((1, 64), 1e-3, np.float16)
+    w = np.ones(64, np.float16)
+    c = float(np.float16(1e-3))
+    assert np.allclose(oq.rms_norm(x, w).astype(np.float64), c / math.sqrt(c * c + 1e-5), rtol=2e-3)
+    assert np.allclose(oq.rms_norm(x, w).astype(np.float64), 0.30151, rtol=2e-3)
+    # alternating signs: mean(x^2) is the same, the signs carry through
+    xs = x * np.where(np.arange(64) % 2 == 0, 1, -1).astype(np.float16)
+    ys = oq.rms_norm(xs, w).astype(np.float64)
+    assert np.allclose(np.abs(ys), 0.30151, rtol=2e-3) and np.all(np.sign(ys) == np.sign(xs))
+    assert np.array_equal(oq.rms_norm(np.zeros((2, 64), np.float16), w), np.zeros((2, 64), np.float16))
+
+
 def test_mlp_block_zero_weights_is_residual_sum():
     rng = np.random.default_rng(5)
     D, I, g = 64, 128, 32
@@ -497,3 +514,28 @@ def test_quantized_verify_attention_is_verify_over_dequantized_pages():
         Kd, Vd = op.dequantize_pages(kq, vq, ks, vs, g, bits, D)
         got = op.quantized_paged_verify_attention(q, kq, vq, ks, vs, bt, [12, 5], g, bits)
         assert np.array_equal(got, op.paged_verify_attention(q, Kd, Vd, bt, [12, 5]))
+
+
+def test_metal_semantics_matvec_one_hot_and_w_rounding():
+    """q4/q8_matvec_w32 (the reference's Metal kernels: fp32 W): a one-hot row
+    e_k gives the fp32 dequant W[n, k] rounded once to fp16 (the dequant's
+    closed form), and on random rows it differs from the pure-array oracle
+    (fp16-rounded W) by no more than the W rounding can move a sum,
+    2^-11 sum_k |x_k W_nk|, plus one output rounding each."""
+    rng = np.random.default_rng(91)
+    N, K, g = 48, 256, 32
+    codes = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
+    s = (rng.standard_normal((N, K // g)) * 0.01).astype(np.float32)
+    z = rng.integers(0, 16, size=(N, K // g)).astype(np.float32)
+    W32 = oq.dequant(codes, s, z, g, np.float32)
+    for k in (0, 1, 97, K - 1):
+        x = np.zeros((1, K), np.float16)
+        x[0, k] = 1.0
+        assert np.array_equal(oq.q4_matvec_w32(x, oq.pack_q4(codes), s, z, g)[0], W32[:, k].astype(np.float16))
+        assert np.array_equal(oq.q8_matvec_w32(x, codes, s, z, g)[0], W32[:, k].astype(np.float16))
+    x = rng.standard_normal((3, K)).astype(np.float16)
+    a = oq.q4_matvec_w32(x, oq.pack_q4(codes), s, z, g).astype(np.float64)
+    b = oq.q4_matvec(x, oq.pack_q4(codes), s, z, g).astype(np.float64)
+    bound = (np.abs(x.astype(np.float64)) @ np.abs(W32.astype(np.float64)).T) * 2.0 ** -11
+    assert np.all(np.abs(a - b) <= bound + (np.abs(a) + np.abs(b)) * 2.0 ** -11 + 1e-7)
+    assert not np.array_equal(a, b)  # the two semantics are distinguishable
