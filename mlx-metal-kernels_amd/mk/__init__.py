@@ -11,6 +11,7 @@ __all__ = [
     "activation_ops",
     "autotune_ops",
     "backend_registry",
+    "decode_block_ops",
     "fused_ops",
     "gqa_ops",
     "kv_cache_ops",

@@ -1,13 +1,16 @@
 """GQA/MQA decode over paged fp16/bf16 KV -- the decode part of
 ``ops/gqa_ops.py`` (prefill attention is outside this package).
 
-The reference has no kernel for paged GQA decode: its
-``paged_gqa_decode_block_from_qkv`` runs split + RoPE with array ops, the
-paged update, and then the pure-array ``reference_paged_gqa_decode_attention``
-(ops/gqa_ops.py:493-547).  Here the whole block is two HIP launches:
+The reference has no kernel for GQA decode: its
+``paged_gqa_decode_block_from_qkv`` (ops/gqa_ops.py:493-547) and
+``gqa_decode_block_from_qkv`` (ops/gqa_ops.py:391-444, contiguous cache) run
+split + RoPE with array ops, the cache update, and then the pure-array
+``reference_*gqa_decode_attention``.  Here each block is two HIP launches:
 ``mk_qkv_rope_paged_update`` (split + interleaved RoPE + in-place paged write)
 and ``mk_paged_decode_attention`` (split-K GQA decode, one K/V read per GQA
-group).  ``paged_gqa_decode_attention`` exposes the attention kernel on its own.
+group); the contiguous cache [B, MAX_S, Hkv, D] goes through both as an
+identity-paged view of the same memory.  ``paged_gqa_decode_attention``
+exposes the attention kernel on its own.
 """
 
 from __future__ import annotations
@@ -16,9 +19,9 @@ import math
 
 import torch
 
-from . import _lib
+from . import _contig, _lib
 from ._common import ACT_DTYPES
-from .kv_cache_ops import normalize_positions
+from .kv_cache_ops import normalize_positions, reference_kv_cache_update
 from .paged_kv_ops import (
     _gather_pages,
     _hip_paged_attention,
@@ -265,3 +268,50 @@ def paged_gqa_decode_block_from_qkv(qkv, K_pages, V_pages, block_table, cos, sin
         scale = 1.0 / math.sqrt(D)
     out = _hip_paged_attention(q_out[:, 0], K_pages, V_pages, bt, pos + 1 if lengths is None else lengths, scale)
     return out.unsqueeze(1).to(qkv.dtype), K_pages, V_pages
+
+
+def reference_gqa_decode_block_from_qkv(qkv, K_cache, V_cache, cos, sin, position, *, num_attention_heads,
+                                        num_key_value_heads, head_dim, scale=None):
+    """ops/gqa_ops.py:345-388: split + RoPE at each sequence's position, the
+    functional contiguous update, and fp32 GQA decode attention over
+    lengths = position + 1."""
+    q_rope, k_rope, v = _per_sequence_rope(qkv, cos, sin, num_attention_heads, num_key_value_heads, head_dim,
+                                           position)
+    updated_K, updated_V = reference_kv_cache_update(K_cache, V_cache, k_rope, v, position)
+    lengths = position + 1 if isinstance(position, int) else normalize_positions(
+        position, qkv.shape[0], K_cache.shape[1], device=K_cache.device) + 1
+    out = reference_gqa_decode_attention(q_rope, updated_K, updated_V, lengths=lengths, scale=scale)
+    return out, updated_K, updated_V
+
+
+def gqa_decode_block_from_qkv(qkv, K_cache, V_cache, cos, sin, position, *, num_attention_heads,
+                              num_key_value_heads, head_dim, scale=None, backend="auto"):
+    """ops/gqa_ops.py:391-444 over a contiguous cache [B, MAX_S, Hkv, D]:
+    the paged block's two launches on an identity-paged view of the cache
+    (no copy).  The new token is written in place and the same tensors are
+    returned as (out [B,1,Hq,D], K_cache, V_cache); the reference returns
+    updated copies that its callers rebind, which reads the same."""
+    backend_name = backend.lower()
+    if backend_name not in ("auto", "reference", "metal", "metal_gqa", "metal_gqa_threadgroup"):
+        raise ValueError("backend must be one of 'reference', 'metal', 'metal_gqa', 'metal_gqa_threadgroup', 'auto'")
+    if backend_name == "reference":
+        return reference_gqa_decode_block_from_qkv(
+            qkv, K_cache, V_cache, cos, sin, position, num_attention_heads=num_attention_heads,
+            num_key_value_heads=num_key_value_heads, head_dim=head_dim, scale=scale)
+    Hq, Hkv, D = num_attention_heads, num_key_value_heads, head_dim
+    validate_gqa_heads(Hq, Hkv)
+    if K_cache.ndim != 4 or V_cache.ndim != 4 or K_cache.shape != V_cache.shape:
+        raise ValueError(f"K_cache and V_cache must be matching [B,MAX_S,H,D], got {tuple(K_cache.shape)}, "
+                         f"{tuple(V_cache.shape)}")
+    B, MAX_S = K_cache.shape[0], K_cache.shape[1]
+    if qkv.shape[0] != B or K_cache.shape[2] != Hkv or K_cache.shape[3] != D:
+        raise ValueError(
+            "k_new and v_new must match cache batch/head/head_dim after normalization. "
+            f"Got qkv={tuple(qkv.shape)} for Hkv={Hkv}, D={D}, cache={tuple(K_cache.shape)}.")
+    dev = _lib.require_device(qkv, K_cache, V_cache)
+    P = _contig.page_size_for(MAX_S)
+    Kp, Vp = _contig.as_pages(K_cache, P), _contig.as_pages(V_cache, P)
+    bt = _contig.identity_table(B, MAX_S, P, dev)
+    out, _, _ = paged_gqa_decode_block_from_qkv(qkv, Kp, Vp, bt, cos, sin, position, num_attention_heads=Hq,
+                                                num_key_value_heads=Hkv, head_dim=D, scale=scale, backend="metal")
+    return out, K_cache, V_cache

@@ -33,10 +33,11 @@ def _validate_inputs(x, cos, sin, position_offset: int):
 
 def reference_apply_rope(x, cos, sin, position_offset: int = 0):
     """ops/rope_ops.py:61-75: pairs (2i, 2i+1) rotate by the angle of row
-    position_offset + s; fp32 math, result in x's dtype."""
+    position_offset + s; fp32 math, result in x's dtype.  The tables may sit
+    on the host: the rows used move to x's device."""
     _, S, _, D, _ = _validate_inputs(x, cos, sin, position_offset)
-    c = cos[position_offset:position_offset + S].to(torch.float32).reshape(1, S, 1, D // 2)
-    s = sin[position_offset:position_offset + S].to(torch.float32).reshape(1, S, 1, D // 2)
+    c = cos[position_offset:position_offset + S].to(device=x.device, dtype=torch.float32).reshape(1, S, 1, D // 2)
+    s = sin[position_offset:position_offset + S].to(device=x.device, dtype=torch.float32).reshape(1, S, 1, D // 2)
     xe = x[..., 0::2].to(torch.float32)
     xo = x[..., 1::2].to(torch.float32)
     ye = xe * c - xo * s
