@@ -18,8 +18,11 @@ carries:
                    HIP events, against the 8 TB/s HBM peak;
   cpu_baseline  -- the numpy oracle (the reference's array path restated)
                    timed on this host for a bounded sample of the same step;
-  extra         -- M=4/8 and q8 variants, and paged GQA decode attention at
-                   BASELINE config 3 (tok/s and HBM fraction).
+  extra         -- M=4/8/32 and q8 variants, paged GQA decode attention at
+                   BASELINE config 3 and at short contexts, config 4 (q8/q4
+                   KV), the speculative-verify attention at config-3 geometry
+                   (W = 2/4/8 rows, MFMA TFLOP/s beside HBM GB/s) and the
+                   config-5 decode stack (tok/s and HBM fraction).
 """
 
 from __future__ import annotations
@@ -42,7 +45,8 @@ TRAFFIC_SUMMARY = "gemv_dot_q4_rmsnorm_gate_up_M1_traffic.json"
 ATTN_TRAFFIC_SUMMARY = "paged_attn_config3_fp16_traffic.json"
 
 
-WORKLOADS = ("config3", "attn_short", "config4", "mlp_m4", "mlp_m8", "mlp_m32", "mlp_q8", "stack")
+WORKLOADS = ("config3", "attn_short", "config4", "verify", "mlp_m4", "mlp_m8", "mlp_m32", "mlp_q8", "stack")
+PEAK_MFMA_F16_TFLOPS = 2500.0  # dense fp16 MFMA peak of MI355X
 
 
 def _parse():
@@ -308,26 +312,83 @@ def attention_config4(dev, steps=30, warmup=5):
     for D in (128, 64):
         for bits in (8, 4):
             cols = D if bits == 8 else D // 2
+            nbytes = B * ctx * Hkv * 2 * (cols + (D // g) * 2)
+            # a cache smaller than 1.5x the 256 MB Infinity Cache is rotated
+            # with further copies, so every call reads its codes from HBM
+            ncopy = max(1, -(-(384 << 20) // nbytes))
             gen = torch.Generator(device=dev)
             gen.manual_seed(7)
-            kq = torch.randint(0, 256, (NP, P, Hkv, cols), dtype=torch.uint8, device=dev, generator=gen)
-            vq = torch.randint(0, 256, (NP, P, Hkv, cols), dtype=torch.uint8, device=dev, generator=gen)
-            ks = (torch.rand((NP, P, Hkv, D // g), device=dev, generator=gen) * 0.2 + 0.05).half()
-            vs = (torch.rand((NP, P, Hkv, D // g), device=dev, generator=gen) * 0.2 + 0.05).half()
             bt = torch.randperm(NP, device=dev, generator=gen).to(torch.int32).reshape(B, mb)
             ln = torch.full((B,), ctx, dtype=torch.int32, device=dev)
-            cache = pq.PagedQuantizedKVCache(k_pages_q=kq, v_pages_q=vq, k_scales=ks, v_scales=vs, block_table=bt,
-                                             lengths=ln, bits=bits, page_size=P, group_size=g,
-                                             original_page_shape=(NP, P, Hkv, D))
+            caches = []
+            for _ in range(ncopy):
+                kq = torch.randint(0, 256, (NP, P, Hkv, cols), dtype=torch.uint8, device=dev, generator=gen)
+                vq = torch.randint(0, 256, (NP, P, Hkv, cols), dtype=torch.uint8, device=dev, generator=gen)
+                ks = (torch.rand((NP, P, Hkv, D // g), device=dev, generator=gen) * 0.2 + 0.05).half()
+                vs = (torch.rand((NP, P, Hkv, D // g), device=dev, generator=gen) * 0.2 + 0.05).half()
+                caches.append(pq.PagedQuantizedKVCache(k_pages_q=kq, v_pages_q=vq, k_scales=ks, v_scales=vs,
+                                                       block_table=bt, lengths=ln, bits=bits, page_size=P,
+                                                       group_size=g, original_page_shape=(NP, P, Hkv, D)))
             q = torch.randn((B, 1, Hq, D), device=dev).half()
-            fns = [lambda: pq.paged_quantized_kv_gqa_decode_attention(q, cache, backend=f"metal_q{bits}")]
-            ms = time_steps(fns, steps, warmup)
-            nbytes = B * ctx * Hkv * 2 * (cols + (D // g) * 2)
+            fns = [lambda c=c: pq.paged_quantized_kv_gqa_decode_attention(q, c, backend=f"metal_q{bits}")
+                   for c in caches]
+            ms = time_steps(fns, max(steps, ncopy), warmup)
             out[f"D{D}_q{bits}"] = {"us_per_call": ms * 1e3, "tokens_per_s": B / (ms * 1e-3),
                                    "hbm_gbs": nbytes / (ms * 1e-3) / 1e9,
-                                   "frac_of_peak": nbytes / (ms * 1e-3) / 1e9 / PEAK_GBS, "bytes": nbytes}
-            del cache, kq, vq, ks, vs, fns
+                                   "frac_of_peak": nbytes / (ms * 1e-3) / 1e9 / PEAK_GBS, "bytes": nbytes,
+                                   "cache_copies": ncopy}
+            del caches, fns
             torch.cuda.empty_cache()
+    return out
+
+
+def attention_verify(dev, steps=60, warmup=10, widths=(2, 4, 8)):
+    """Speculative verify at config-3 geometry: B=16, Hq 32 / Hkv 8, D=128,
+    P=16, lengths U[512, 8192] (seed 3, counting the W drafts), W draft
+    rows per sequence.  mk_paged_verify_attention reads each K/V byte once
+    for the W rows (W * 4 MFMA columns per kv head); for comparison the
+    same rows run as B * W sequences of the decode kernel sharing their
+    table rows (the KV read W times).  Two cache copies of >= 256 MB rotate.
+    Bytes = KV of every position read once + q and out; MFMA work = the
+    QK^T and PV products of every row over its visible positions."""
+    import numpy as np
+    import torch
+
+    import mk.gqa_ops as gqa
+    import mk.speculative_verify_ops as sv
+
+    B, Hq, Hkv, D, P, mb = 16, 32, 8, 128, 16, 512
+    lengths = np.random.default_rng(3).integers(512, 8193, size=B).astype(np.int32)
+    NP = B * mb
+    bt = torch.from_numpy(np.random.default_rng(4).permutation(NP).astype(np.int32).reshape(B, mb)).to(dev)
+    ln = torch.from_numpy(lengths).to(dev)
+    caches = [(torch.randn((NP, P, Hkv, D), device=dev).to(torch.float16),
+               torch.randn((NP, P, Hkv, D), device=dev).to(torch.float16)) for _ in range(2)]
+    tot = int(lengths.sum())
+    out = {"workload": "verify_paged_gqa_fp16_B16_ctx_U512_8192"}
+    for W in widths:
+        q = torch.randn((B, W, Hq, D), device=dev).to(torch.float16)
+        fns = [lambda K=K, V=V: sv.paged_verify_attention(q, K, V, bt, ln) for K, V in caches]
+        ms = time_steps(fns, steps, warmup)
+        # the W rows as B * W decode sequences (row w: length - (W - 1 - w))
+        rows_bt = bt.repeat_interleave(W, dim=0)
+        rows_ln = (ln[:, None] - torch.arange(W - 1, -1, -1, device=dev, dtype=torch.int32)[None, :]).reshape(-1)
+        q3 = q.reshape(B * W, 1, Hq, D)
+        fr = [lambda K=K, V=V: gqa.paged_gqa_decode_attention(q3, K, V, rows_bt, rows_ln) for K, V in caches]
+        ms_rows = time_steps(fr, steps, warmup)
+        nbytes = tot * Hkv * D * 2 * 2 + sum(-(-int(n) // P) for n in lengths) * 4 + B * W * Hq * D * 2 * 2 + B * 4
+        vis = sum(int(n) - (W - 1 - w) for n in lengths for w in range(W))  # positions seen, over all rows
+        flops = 4.0 * vis * Hq * D
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        tfl = flops / (ms * 1e-3) / 1e12
+        out[f"W{W}"] = {"us_per_call": round(ms * 1e3, 3), "tokens_per_s": B * W / (ms * 1e-3),
+                        "hbm_gbs": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4), "bytes": nbytes,
+                        "mfma_tflops": round(tfl, 2), "mfma_frac": round(tfl / PEAK_MFMA_F16_TFLOPS, 5),
+                        "rows_as_sequences_us": round(ms_rows * 1e3, 3),
+                        "speedup_vs_rows_as_sequences": round(ms_rows / ms, 3)}
+        del fns, fr, q, q3, rows_bt, rows_ln
+    del caches
+    torch.cuda.empty_cache()
     return out
 
 
@@ -678,6 +739,8 @@ def run_workload(name, dev, args):
         return attention_config3(dev, max(50, args.steps // 3), 10)
     if name == "config4":
         return attention_config4(dev)
+    if name == "verify":
+        return attention_verify(dev)
     if name == "attn_short":
         return {"workload": "paged_gqa_fp16_short_contexts", **attention_short(dev)}
     if name == "stack":
@@ -755,6 +818,7 @@ def main():
         extra["paged_attention"] = attention_config3(dev, max(50, args.steps // 3), 10)
         extra["paged_attention_short"] = attention_short(dev)
         extra["quantized_attention"] = attention_config4(dev)
+        extra["verify_attention"] = attention_verify(dev)
         extra["decode_stack"] = decode_stack_config5(dev)
 
     cpu = None

@@ -305,6 +305,31 @@ int mk_paged_quantized_decode_attention(const void* q, const uint8_t* K_q, const
                                         int64_t group_size, int bits, float scale, int dtype,
                                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Speculative-verify attention: W draft rows per sequence in one pass over
+ * the cache -- the attention of the staged verify loop
+ * (ops/speculative_verify_ops.py:228-262, each step a paged GQA decode,
+ * ops/gqa_ops.py:307-342).  q and out [B, W, Hq, D]; lengths [B] count the
+ * context and all W new positions; row w sees positions
+ * < lengths[b] - (W - 1 - w) (none: zeros).  The W * Hq/Hkv rows of one kv
+ * head are the columns of one MFMA contraction, so each K/V byte is read
+ * once for all W rows.  Workspace: mk_paged_attention_workspace_bytes(B,
+ * W * Hq, Hkv, D, max_blocks, page_size).  1 <= W <= 64. */
+int mk_paged_verify_attention(const void* q, const void* K_pages, const void* V_pages,
+                              const int32_t* block_table, const int32_t* lengths, void* out,
+                              int64_t B, int64_t W, int64_t Hq, int64_t Hkv, int64_t D, int64_t page_size,
+                              int64_t max_blocks, int64_t num_pages, float scale, int dtype,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/* mk_paged_verify_attention over q8/q4 pages (layout as
+ * mk_paged_quantized_decode_attention). */
+int mk_paged_quantized_verify_attention(const void* q, const uint8_t* K_q, const uint8_t* V_q,
+                                        const f16_storage_t* K_s, const f16_storage_t* V_s,
+                                        const int32_t* block_table, const int32_t* lengths, void* out,
+                                        int64_t B, int64_t W, int64_t Hq, int64_t Hkv, int64_t D,
+                                        int64_t page_size, int64_t max_blocks, int64_t num_pages,
+                                        int64_t group_size, int bits, float scale, int dtype,
+                                        void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,7 +66,8 @@ constexpr int kMaxSegs = 64;
 constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
 
 // One segment of a pair: sequence, first and end position, page-list index
-// of its first page (bit 30: the segment is the whole sequence).
+// of its first page (bit 30: the segment is the whole sequence).  (Verify
+// kernels keep each segment's sequence length in a parallel LDS array.)
 struct SegDesc {
   int b, t0, t1, po;
 };
@@ -104,7 +105,60 @@ struct PagedArgs {
   int sp_blk, sp_nw, sp_nwg;
   int* cnt;            // arrival counters [B][units], zero between calls
   float scale_log2;
+  // verify width: query rows per sequence (1 for decode).  With vw = W the
+  // kernels see W * Hq "virtual heads" v = h * W + w per sequence (so a kv
+  // head's W * G rows are consecutive, like its GQA group in decode), row w
+  // seeing positions < length - (W - 1 - w); q and out stay [B, W, Hq, D]
+  int vw;
+  int vw_magic;        // ceil(2^16 / vw), see vsplit
 };
+
+// Row of q / out that holds virtual head v of sequence b: [B, Hq, D] in
+// decode; [B, W, Hq / W, D] with v = h * W + w for verify rows.  (The merge
+// and generic kernels use this; the attention kernels use qo_row_j below.)
+__device__ __forceinline__ size_t qo_row(const PagedArgs& a, int b, int v) {
+  if (a.vw <= 1) return (size_t)b * a.Hq + v;
+  const int h = v / a.vw, w = v - h * a.vw;
+  return ((size_t)b * a.vw + w) * (size_t)(a.Hq / a.vw) + h;
+}
+
+// Verify kernels: the virtual heads a wave touches are h0 + j, j < 16, for
+// its wave-uniform h0 = hq0 * W + hr0.  (h0 + j) / W = hq0 + x / W with
+// x = hr0 + j < W + 16 <= 80, and x / W = (x * vw_magic) >> 16 exactly for
+// vw_magic = ceil(2^16 / W), W <= 64 (the rounding error x (W - 1) / 2^16 W
+// stays below the 1 / W gap to the next integer) -- no division per lane.
+struct VRows {
+  int hq0, hr0;
+};
+__device__ __forceinline__ VRows vrows(const PagedArgs& a, int h0) {
+  const int q = h0 / a.vw;  // wave-uniform, once per wave
+  return VRows{q, h0 - q * a.vw};
+}
+// row w of virtual head h0 + j and its head index h
+__device__ __forceinline__ void vsplit(const PagedArgs& a, VRows r, int j, int* h, int* w) {
+  const int x = r.hr0 + j;
+  const int qd = (x * a.vw_magic) >> 16;
+  *w = x - qd * a.vw;
+  *h = r.hq0 + qd;
+}
+// row of q / out for virtual head h0 + j of sequence b (verify: 32-bit
+// arithmetic, the host keeps B * W * Hq below 2^31)
+template <bool VW>
+__device__ __forceinline__ size_t qo_row_j(const PagedArgs& a, VRows r, int b, int h0, int j) {
+  if constexpr (!VW) {
+    return (size_t)b * a.Hq + h0 + j;
+  } else {
+    int h, w;
+    vsplit(a, r, j, &h, &w);
+    return (size_t)(uint32_t)((b * a.vw + w) * (a.Hq / a.vw) + h);
+  }
+}
+
+// Positions before a sequence's end that virtual head v may not see: W - 1 - w
+// for verify row w, 0 in decode.
+__device__ __forceinline__ int causal_offset(const PagedArgs& a, int v) {
+  return a.vw <= 1 ? 0 : a.vw - 1 - v % a.vw;
+}
 
 // --------------------------------------------------------------- MFMA wrappers
 template <typename AT>
@@ -280,6 +334,9 @@ struct KVBlock {
   u32x4 v[8];
   uint32_t vs[8];
   uint32_t mask;  // bit p: position p of the block is valid (wave-uniform)
+  // positions from the block's first to its sequence's end (wave-uniform):
+  // verify row w may see block positions p < rel_end - (W - 1 - w)
+  int rel_end;
 };
 
 // ------------------------------------------------------------ stream plan
@@ -477,7 +534,7 @@ __device__ void merge_heads(const PagedArgs& a, int b, int h0, int hcount, int f
         }
       }
       const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-      AT* op = reinterpret_cast<AT*>(a.out) + ((size_t)b * a.Hq + h) * D + lane * DPT;
+      AT* op = reinterpret_cast<AT*>(a.out) + qo_row(a, b, h) * D + lane * DPT;
       if constexpr (DPT == 2) {
         *reinterpret_cast<uint32_t*>(op) = pack_act2<AT>(acc[0] * inv, acc[1] * inv);
       } else {
@@ -532,7 +589,7 @@ __device__ void merge_heads(const PagedArgs& a, int b, int h0, int hcount, int f
     }
     L = wave_sum(L);
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    AT* op = reinterpret_cast<AT*>(a.out) + ((size_t)b * a.Hq + h) * D + lane * DPT;
+    AT* op = reinterpret_cast<AT*>(a.out) + qo_row(a, b, h) * D + lane * DPT;
     if constexpr (DPT == 2) {
       *reinterpret_cast<uint32_t*>(op) = pack_act2<AT>(acc[0] * inv, acc[1] * inv);
     } else {
@@ -554,7 +611,7 @@ __global__ __launch_bounds__(64) void paged_attn_merge_kernel(const PagedArgs a)
   int64_t start;
   seq_info(a, sp, b, lane, &len, &start);
   if (len == 0) {
-    AT* op = reinterpret_cast<AT*>(a.out) + ((size_t)b * a.Hq + h) * D;
+    AT* op = reinterpret_cast<AT*>(a.out) + qo_row(a, b, h) * D;
     for (int d = lane; d < D; d += 64) op[d] = from_f32<AT>(0.0f);
     return;
   }
@@ -577,6 +634,7 @@ struct SplitCtx {
   int blk0;          // logical page of the segment's first position
   int po;            // list index of that page
   int t_begin, t_end, lgP, Pm, Hkv, hkv;
+  int seq_len;       // length of the segment's sequence
   // !PT: row index (page, slot, kv head) of position t, clamped into the
   // segment; *ok says whether t is a real, mapped position
   __device__ __forceinline__ uint32_t row(int t, bool* ok) const {
@@ -691,6 +749,7 @@ __device__ __forceinline__ void load_block(KVBlock<KVF, D, SB>& blk, const Paged
       }
     }
     blk.mask = m;
+    blk.rel_end = c.seq_len - tb;
   } else {
     uint32_t m = 0;
 #pragma unroll
@@ -739,6 +798,7 @@ __device__ __forceinline__ void load_block(KVBlock<KVF, D, SB>& blk, const Paged
       if constexpr (KVF != 0)
         blk.vs[p] = a.Vs[(uint64_t)row * a.ngroups + ((r16 * F::DPL) >> a.lg_gs)];
     }
+    blk.rel_end = c.seq_len - tb;
   }
 }
 
@@ -809,17 +869,17 @@ __device__ __forceinline__ void set_segment(SplitCtx& c, const SegDesc d) {
 // 1 .. kQSlots-1, then the segment list.
 template <int D>
 __host__ __device__ constexpr size_t attn_wave_lds() {
-  return (size_t)(kQSlots - 1) * (D / 32) * 64 * 16 + kMaxSegs * sizeof(SegDesc);
+  return (size_t)(kQSlots - 1) * (D / 32) * 64 * 16 + kMaxSegs * (sizeof(SegDesc) + sizeof(int));
 }
 
 // q^T operand of sequence b: lane (head r16, kb) gets q[b, h0 + r16][dbase(j, kb) .. +8]
 // (zeros for heads past hcount), in the K dequant order.
-template <typename AT, int D, int KVF>
-__device__ __forceinline__ void load_q(const PagedArgs& a, int b, int h0, int hcount, int r16, int kb,
+template <typename AT, int D, int KVF, bool VW>
+__device__ __forceinline__ void load_q(const PagedArgs& a, VRows vr, int b, int h0, int hcount, int r16, int kb,
                                        u32x4* qv) {
   using F = Fmt<KVF, D>;
   const bool hv = r16 < hcount;
-  const AT* qp = reinterpret_cast<const AT*>(a.q) + ((size_t)b * a.Hq + h0 + (hv ? r16 : 0)) * D;
+  const AT* qp = reinterpret_cast<const AT*>(a.q) + qo_row_j<VW>(a, vr, b, h0, hv ? r16 : 0) * D;
 #pragma unroll
   for (int j = 0; j < F::KSTEPS; ++j) {
     const u32x4 x = ldg128(qp + F::dbase(j, kb));
@@ -828,29 +888,31 @@ __device__ __forceinline__ void load_q(const PagedArgs& a, int b, int h0, int hc
 }
 
 // q of segment s >= 1: from its LDS slot, or (past kQSlots) from global memory.
-template <typename AT, int D, int KVF>
-__device__ __forceinline__ void begin_segment(const PagedArgs& a, u32x4* qv, const u32x4* qslots, int s,
+template <typename AT, int D, int KVF, bool VW>
+__device__ __forceinline__ void begin_segment(const PagedArgs& a, VRows vr, u32x4* qv, const u32x4* qslots, int s,
                                               const SegDesc* sd, int h0, int hcount, int lane, int r16, int kb) {
   constexpr int KSTEPS = Fmt<KVF, D>::KSTEPS;
   if (s < kQSlots) {
 #pragma unroll
     for (int j = 0; j < KSTEPS; ++j) qv[j] = qslots[((s - 1) * KSTEPS + j) * 64 + lane];
   } else {
-    load_q<AT, D, KVF>(a, seg_at(sd, s).b, h0, hcount, r16, kb, qv);
+    load_q<AT, D, KVF, VW>(a, vr, seg_at(sd, s).b, h0, hcount, r16, kb, qv);
   }
 }
 
 // Write segment s's result: the output when the segment is its whole
 // sequence, else the partial (O unnormalised, m, l) in slot pair + b.
 // Lane holds O[head 4kb + i][d = r16*DPL + vslot(j)].
-template <typename AT, int D, int KVF>
-__device__ __forceinline__ void write_segment(const PagedArgs& a, const f32x4* o, float m_run, float l_run,
-                                              const SegDesc d, int pair, int h0, int hcount) {
+template <typename AT, int D, int KVF, bool VW>
+__device__ __forceinline__ void write_segment(const PagedArgs& a, VRows vr, const f32x4* o, float m_run,
+                                              float l_run, const SegDesc d, int pair, int h0, int hcount) {
   using F = Fmt<KVF, D>;
   constexpr int DPL = F::DPL;
   // lane-derived values are recomputed here so they need not stay live
-  // across the block loop
-  const int lane = (int)__lane_id();
+  // across the block loop (verify kernels: an opaque lane index, so the
+  // compiler cannot hoist the rows' address arithmetic out of the loop)
+  int lane = (int)__lane_id();
+  if constexpr (VW) asm volatile("" : "+v"(lane));
   const int r16 = lane & 15, kb = lane >> 4;
   const int b = d.b;
   const bool whole = (d.po >> 30) & 1;
@@ -872,7 +934,7 @@ __device__ __forceinline__ void write_segment(const PagedArgs& a, const f32x4* o
       uint32_t w[DPL / 2];
 #pragma unroll
       for (int e = 0; e < DPL / 2; ++e) w[e] = pack_act2<AT>(nat[2 * e] * inv, nat[2 * e + 1] * inv);
-      AT* op = reinterpret_cast<AT*>(a.out) + ((size_t)b * a.Hq + h0 + h) * D + r16 * DPL;
+      AT* op = reinterpret_cast<AT*>(a.out) + qo_row_j<VW>(a, vr, b, h0, h) * D + r16 * DPL;
       if constexpr (DPL == 8) *reinterpret_cast<u32x4*>(op) = (u32x4){w[0], w[1], w[2], w[3]};
       else *reinterpret_cast<u32x2*>(op) = (u32x2){w[0], w[1]};
     } else {
@@ -895,11 +957,11 @@ constexpr float kLazyMax = 8.0f;
 // 16-position tiles, the (lazy) running max and sum, O += P V.  Lane
 // (r16, kb) holds m_run / l_run of head r16 and O[head 4kb + i][d slot j] in
 // o[j][i]; masked positions get p = 0 and a zeroed V row.
-template <typename AT, int D, int KVF, bool SB>
+template <typename AT, int D, int KVF, bool SB, bool VW>
 __device__ __forceinline__ void consume_block(const KVBlock<KVF, D, SB> blk,
                                               const u32x4 (&qv)[Fmt<KVF, D>::KSTEPS], float scale_log2,
-                                              int kb, float& m_run, float& l_run,
-                                              f32x4 (&o)[Fmt<KVF, D>::DPL]) {
+                                              int kb, const PagedArgs& a, VRows vr, float& m_run,
+                                              float& l_run, f32x4 (&o)[Fmt<KVF, D>::DPL]) {
   constexpr int KSTEPS = Fmt<KVF, D>::KSTEPS;
   constexpr int DPL = Fmt<KVF, D>::DPL;
   // ---- S^T = K q^T for the two 16-position tiles
@@ -918,12 +980,24 @@ __device__ __forceinline__ void consume_block(const KVBlock<KVF, D, SB> blk,
 #pragma unroll
     for (int i = 0; i < 4; ++i) sv[u][i] = sc[u][i] * scale_log2;
   const bool full = blk.mask == 0xFFFFFFFFu;  // wave-uniform
-  if (!full) {
+  // verify rows: a row's causal limit inside this block (wave-uniform test)
+  const bool climit = VW && blk.rel_end - (a.vw - 1) < kBlockPos;
+  if (!full || climit) {
+    uint32_t mk = blk.mask;
+    if (climit) {
+      // lane column r16 is virtual head h0 + r16 = h * W + w, which sees
+      // block positions < rel_end - (W - 1 - w); folded into the mask here,
+      // in the few blocks that need it, so nothing stays live across the loop
+      int hh, w;
+      vsplit(a, vr, (int)__lane_id() & 15, &hh, &w);
+      const int lim = blk.rel_end - (a.vw - 1 - w);
+      mk &= lim >= kBlockPos ? 0xFFFFFFFFu : (lim <= 0 ? 0u : (1u << lim) - 1u);
+    }
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (!((blk.mask >> (16 * u + 4 * kb + i)) & 1u)) sv[u][i] = -INFINITY;
+        if (!((mk >> (16 * u + 4 * kb + i)) & 1u)) sv[u][i] = -INFINITY;
   }
   float bmax = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
                      fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
@@ -989,7 +1063,7 @@ __device__ __forceinline__ void consume_block(const KVBlock<KVF, D, SB> blk,
   }
 }
 
-template <typename AT, int D, int KVF, bool SB, bool PT>
+template <typename AT, int D, int KVF, bool SB, bool PT, bool VW>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void paged_attn_kernel(
     const PagedArgs a) {
   using F = Fmt<KVF, D>;
@@ -1026,6 +1100,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   extern __shared__ __align__(16) uint8_t attn_dyn[];
   u32x4* qslots = reinterpret_cast<u32x4*>(attn_dyn + (size_t)(threadIdx.x >> 6) * attn_wave_lds<D>());
   SegDesc* sd = reinterpret_cast<SegDesc*>(qslots + (kQSlots - 1) * KSTEPS * 64);
+  int* slen = reinterpret_cast<int*>(sd + kMaxSegs);  // verify: segment s's sequence length
+  const VRows vr = VW ? vrows(a, h0) : VRows{0, 0};
   int nseg = 0, npg = 0;
   {
     int64_t st;
@@ -1039,7 +1115,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       const int lbe = (int)((int64_t)nb < g1 - st ? (int64_t)nb : g1 - st);
       const int t0 = lbb * kBlockPos;
       const int t1 = min(lbe * kBlockPos, len);
-      if (lane == 0) sd[nseg] = SegDesc{b, t0, t1, npg | ((lbb == 0 && lbe == nb) ? (1 << 30) : 0)};
+      if (lane == 0) {
+        sd[nseg] = SegDesc{b, t0, t1, npg | ((lbb == 0 && lbe == nb) ? (1 << 30) : 0)};
+        if constexpr (VW) slen[nseg] = len;
+      }
       npg += ((t1 - 1) >> a.lgP) - (t0 >> a.lgP) + 1;
       ++nseg;
       g = st + lbe;
@@ -1052,10 +1131,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   // Lane (head r16, kb) holds q[h0 + r16][dbase(j, kb) .. +8] for step j.
   u32x4 qv[KSTEPS];
   u32x4 qx[kQSlots > 1 ? kQSlots - 1 : 1][KSTEPS];
-  load_q<AT, D, KVF>(a, seg_at(sd, 0).b, h0, hcount, r16, kb, qv);
+  load_q<AT, D, KVF, VW>(a, vr, seg_at(sd, 0).b, h0, hcount, r16, kb, qv);
 #pragma unroll
   for (int s = 1; s < kQSlots; ++s)
-    load_q<AT, D, KVF>(a, seg_at(sd, s < nseg ? s : 0).b, h0, hcount, r16, kb, qx[s - 1]);
+    load_q<AT, D, KVF, VW>(a, vr, seg_at(sd, s < nseg ? s : 0).b, h0, hcount, r16, kb, qx[s - 1]);
 
   __shared__ int spage[PT ? 1 : kMaxSplitPages];
   SplitCtx c;
@@ -1088,7 +1167,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   for (int j = 0; j < DPL; ++j) o[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   auto consume = [&](const Blk& blk) {
-    consume_block<AT, D, KVF, SB>(blk, qv, a.scale_log2, kb, m_run, l_run, o);
+    consume_block<AT, D, KVF, SB, VW>(blk, qv, a.scale_log2, kb, a, vr, m_run, l_run, o);
   };
 
   // Blocks 2k and 2k+1 of the pair stream through buffers A and B.  Each
@@ -1114,9 +1193,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     for (int q = 0; q < 8; ++q) Bq.vs[q] = 0u;
   }
   Bq.mask = 0u;
+  Bq.rel_end = 1 << 30;
 
   int segL = 0, jL0 = 0, jL1 = 0;  // load side: segment, its first and end pair-local block
+  auto seg_len = [&](int sgi) {
+    if constexpr (VW) c.seq_len = __builtin_amdgcn_readfirstlane(slen[sgi]);
+  };
   set_segment(c, seg_at(sd, 0));
+  seg_len(0);
   jL1 = nblk_of(c.t_end - c.t_begin);
   int segC = 0, jC1 = jL1;         // consume side: segment and its end block
 
@@ -1125,6 +1209,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       ++segL;
       jL0 = jL1;
       set_segment(c, seg_at(sd, segL));
+      seg_len(segL);
       jL1 = jL0 + nblk_of(c.t_end - c.t_begin);
     }
     load_block<AT, D, KVF, SB, PT>(A, a, c, lo, c.t_begin + kBlockPos * (i - jL0), r16, kb);
@@ -1135,19 +1220,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       ++segL;
       jL0 = jL1;
       set_segment(c, seg_at(sd, segL));
+      seg_len(segL);
       jL1 = jL0 + nblk_of(c.t_end - c.t_begin);
     }
     load_block<AT, D, KVF, SB, PT>(Bq, a, c, lo, c.t_begin + kBlockPos * ((has1 ? i + 1 : i) - jL0), r16, kb);
     if (!has1) Bq.mask = 0u;
     __builtin_amdgcn_sched_barrier(0);
     if (i >= jC1) {  // wave-uniform: block i opens the next segment
-      write_segment<AT, D, KVF>(a, o, m_run, l_run, seg_at(sd, segC), pair, h0, hcount);
+      write_segment<AT, D, KVF, VW>(a, vr, o, m_run, l_run, seg_at(sd, segC), pair, h0, hcount);
       ++segC;
       {
         const SegDesc d = seg_at(sd, segC);
         jC1 += nblk_of(d.t1 - d.t0);
       }
-      begin_segment<AT, D, KVF>(a, qv, qslots, segC, sd, h0, hcount, lane, r16, kb);
+      begin_segment<AT, D, KVF, VW>(a, vr, qv, qslots, segC, sd, h0, hcount, lane, r16, kb);
       m_run = -INFINITY;
       l_run = 0.0f;
 #pragma unroll
@@ -1155,13 +1241,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     }
     consume(A);
     if (has1 && i + 1 >= jC1) {  // wave-uniform: block i + 1 (consumed next trip) opens the next segment
-      write_segment<AT, D, KVF>(a, o, m_run, l_run, seg_at(sd, segC), pair, h0, hcount);
+      write_segment<AT, D, KVF, VW>(a, vr, o, m_run, l_run, seg_at(sd, segC), pair, h0, hcount);
       ++segC;
       {
         const SegDesc d = seg_at(sd, segC);
         jC1 += nblk_of(d.t1 - d.t0);
       }
-      begin_segment<AT, D, KVF>(a, qv, qslots, segC, sd, h0, hcount, lane, r16, kb);
+      begin_segment<AT, D, KVF, VW>(a, vr, qv, qslots, segC, sd, h0, hcount, lane, r16, kb);
       m_run = -INFINITY;
       l_run = 0.0f;
 #pragma unroll
@@ -1169,7 +1255,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     }
   }
   consume(Bq);  // the last odd block (or an empty one)
-  write_segment<AT, D, KVF>(a, o, m_run, l_run, seg_at(sd, segC), pair, h0, hcount);
+  write_segment<AT, D, KVF, VW>(a, vr, o, m_run, l_run, seg_at(sd, segC), pair, h0, hcount);
 }
 
 // ------------------------------------------------------- short-context plan
@@ -1230,7 +1316,7 @@ constexpr int64_t kSpShortRowBlocks = 128;
 constexpr int64_t kSpWaves = MK_ATTN_SP_WAVES;          // waves it aims for (one round on 256 CUs)
 constexpr int kSpMergeTrip = 16;                        // partials the final merge reads per trip
 
-template <typename AT, int D, int KVF, bool SB>
+template <typename AT, int D, int KVF, bool SB, bool VW>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void paged_attn_sp_kernel(
     const PagedArgs a) {
   using F = Fmt<KVF, D>;
@@ -1256,11 +1342,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   const int max_s = a.MB << a.lgP;
   const int span = a.sp_blk * kBlockPos;     // positions per split
   const int t0 = (wgi * nw + wave) * span;  // this wave's first position
+  const VRows vr = VW ? vrows(a, h0) : VRows{0, 0};
 
   // ---- requested together: the length, q and the split's page ids
   const int len = clamp_len(a.lengths[b], max_s);
   u32x4 qv[KSTEPS];
-  load_q<AT, D, KVF>(a, b, h0, hcount, r16, kb, qv);
+  load_q<AT, D, KVF, VW>(a, vr, b, h0, hcount, r16, kb, qv);
   const int pg0 = t0 >> a.lgP;
   int my_page = -1;
   {
@@ -1274,8 +1361,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   const int nwg = (nsplit + nw - 1) / nw;                       // workgroups holding positions
   if (wgi >= nwg) {  // workgroup-uniform
     if (wgi == 0) {  // empty sequence
-      AT* op = reinterpret_cast<AT*>(a.out) + ((size_t)b * a.Hq + h0) * D;
-      for (int i = threadIdx.x; i < hcount * D; i += blockDim.x) op[i] = from_f32<AT>(0.0f);
+      for (int i = threadIdx.x; i < hcount * D; i += blockDim.x)
+        reinterpret_cast<AT*>(a.out)[qo_row_j<VW>(a, vr, b, h0, i / D) * D + i % D] = from_f32<AT>(0.0f);
     }
     return;
   }
@@ -1293,6 +1380,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   c.Pm = (1 << a.lgP) - 1;
   c.Hkv = a.Hkv;
   c.hkv = hkv;
+  c.seq_len = len;
   const LaneOffsets<KVF, D, SB> lo = pt_lane_offsets<KVF, D, SB>(a, r16, kb);
 
   float m_run = -INFINITY;  // per head r16 (replicated over kb)
@@ -1301,7 +1389,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
   for (int j = 0; j < DPL; ++j) o[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
   auto consume = [&](const Blk& blk) {
-    consume_block<AT, D, KVF, SB>(blk, qv, a.scale_log2, kb, m_run, l_run, o);
+    consume_block<AT, D, KVF, SB, VW>(blk, qv, a.scale_log2, kb, a, vr, m_run, l_run, o);
   };
 
   // Blocks stream through buffers A and B, each refilled right after it is
@@ -1330,6 +1418,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       for (int q = 0; q < 8; ++q) Bq.vs[q] = 0u;
     }
     Bq.mask = 0u;
+    Bq.rel_end = 1 << 30;
     for (int i = 0; i < nbt; i += 2) {
       load_block<AT, D, KVF, SB, true>(A, a, c, lo, t0 + kBlockPos * i, r16, kb);
       __builtin_amdgcn_sched_barrier(0);
@@ -1367,7 +1456,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
   const bool single = nwg == 1;  // workgroup-uniform
   // partial (g) of head h0 + h: row ((b * Hq + h0 + h) * sp_nwg + g)
   const size_t prow = ((size_t)b * a.Hq + h0) * a.sp_nwg;
-  AT* out = reinterpret_cast<AT*>(a.out) + ((size_t)b * a.Hq + h0) * D;
+  AT* const outp = reinterpret_cast<AT*>(a.out);
   for (int it = threadIdx.x; it < hcount * D; it += blockDim.x) {
     const int h = it / D;
     const int d = it - h * D;
@@ -1381,7 +1470,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
       O += so[(size_t)(w * hcount + h) * D + d] * e;
     }
     if (single) {
-      out[it] = from_f32<AT>(O * (L > 0.0f ? 1.0f / L : 0.0f));
+      outp[qo_row_j<VW>(a, vr, b, h0, h) * D + d] = from_f32<AT>(O * (L > 0.0f ? 1.0f / L : 0.0f));
     } else {
       const size_t row = prow + (size_t)h * a.sp_nwg + wgi;
       store_agent(a.ws + row * D + d, O);
@@ -1474,7 +1563,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     }
     if (sub == 0) {
       const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-      *reinterpret_cast<u32x2*>(out + h * D + 4 * dv) =
+      *reinterpret_cast<u32x2*>(outp + qo_row_j<VW>(a, vr, b, h0, h) * D + 4 * dv) =
           (u32x2){pack_act2<AT>(O[0] * inv, O[1] * inv), pack_act2<AT>(O[2] * inv, O[3] * inv)};
     }
   }
@@ -1492,7 +1581,9 @@ __global__ __launch_bounds__(64) void paged_attn_generic_kernel(const PagedArgs 
   int len = a.lengths[b];
   const int max_s = a.MB * a.P;
   len = len < 0 ? 0 : (len > max_s ? max_s : len);
-  const AT* qp = reinterpret_cast<const AT*>(a.q) + (size_t)bh * D;
+  len -= causal_offset(a, h);  // a verify row's causal limit
+  const size_t qrow = qo_row(a, b, h);
+  const AT* qp = reinterpret_cast<const AT*>(a.q) + qrow * D;
   constexpr int MAXPL = 4;  // D <= 256
   float qr[MAXPL], acc[MAXPL];
 #pragma unroll
@@ -1550,7 +1641,7 @@ __global__ __launch_bounds__(64) void paged_attn_generic_kernel(const PagedArgs 
     for (int k = 0; k < MAXPL; ++k) acc[k] = acc[k] * alpha + p * vv[k];
   }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  AT* op = reinterpret_cast<AT*>(a.out) + (size_t)bh * D;
+  AT* op = reinterpret_cast<AT*>(a.out) + qrow * D;
 #pragma unroll
   for (int k = 0; k < MAXPL; ++k) {
     const int d = threadIdx.x + 64 * k;
@@ -1695,7 +1786,11 @@ int attention_launch(PagedArgs a, int64_t D, int kvf, int dtype, size_t ws_bytes
       const dim3 grid((unsigned)((int64_t)a.sp_nwg * a.B * a.units));
       const dim3 block(64u * (unsigned)a.sp_nw);
       const size_t lds = sp_lds_bytes(a, a.sp_nw, D);
-#define MK_SP(AT, DD, KF, SB) paged_attn_sp_kernel<AT, DD, KF, SB><<<grid, block, lds, st>>>(a)
+#define MK_SP(AT, DD, KF, SB)                                                        \
+  do {                                                                               \
+    if (a.vw > 1) paged_attn_sp_kernel<AT, DD, KF, SB, true><<<grid, block, lds, st>>>(a);   \
+    else paged_attn_sp_kernel<AT, DD, KF, SB, false><<<grid, block, lds, st>>>(a);           \
+  } while (0)
       if (kvf == 0) {
         if (dtype == MK_DT_F16) {
           if (D == 128) MK_SP(f16, 128, 0, false); else MK_SP(f16, 64, 0, false);
@@ -1725,8 +1820,13 @@ int attention_launch(PagedArgs a, int64_t D, int kvf, int dtype, size_t ws_bytes
     const size_t qlds = (size_t)a.wg_units * (D == 128 ? attn_wave_lds<128>() : attn_wave_lds<64>());
 #define MK_PA2(AT, DD, KF, SB)                                                               \
   do {                                                                                      \
-    if (a.P % 16 == 0) paged_attn_kernel<AT, DD, KF, SB, true><<<grid, block, qlds, st>>>(a); \
-    else paged_attn_kernel<AT, DD, KF, SB, false><<<grid, block, qlds, st>>>(a);            \
+    if (a.vw > 1) {                                                                         \
+      if (a.P % 16 == 0) paged_attn_kernel<AT, DD, KF, SB, true, true><<<grid, block, qlds, st>>>(a); \
+      else paged_attn_kernel<AT, DD, KF, SB, false, true><<<grid, block, qlds, st>>>(a);            \
+    } else {                                                                                \
+      if (a.P % 16 == 0) paged_attn_kernel<AT, DD, KF, SB, true, false><<<grid, block, qlds, st>>>(a); \
+      else paged_attn_kernel<AT, DD, KF, SB, false, false><<<grid, block, qlds, st>>>(a);            \
+    }                                                                                       \
   } while (0)
 #define MK_PA(AT, DD, KF, SB) MK_PA2(AT, DD, KF, SB)
     if (kvf == 0) {
@@ -1806,6 +1906,41 @@ int fp16_args(PagedArgs& a, const void* q, const void* K_pages, const void* V_pa
   a.gs = 1;
   a.ngroups = 1;
   a.scale_log2 = scale * kLog2e;
+  a.vw = 1;
+  return MK_OK;
+}
+
+// Argument checks and PagedArgs set-up shared by the q8/q4 entry points.
+int quant_args(PagedArgs& a, const void* q, const uint8_t* K_q, const uint8_t* V_q, const f16_storage_t* K_s,
+               const f16_storage_t* V_s, const int32_t* block_table, const int32_t* lengths, void* out,
+               int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t page_size, int64_t max_blocks,
+               int64_t num_pages, int64_t group_size, int bits, float scale, int dtype) {
+  MK_REQUIRE(q && K_q && V_q && K_s && V_s && block_table && lengths && out);
+  MK_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && (Hq % Hkv) == 0 && D > 0 && page_size > 0);
+  MK_REQUIRE(max_blocks > 0 && num_pages > 0 && num_pages < (1LL << 31) && group_size > 0);
+  MK_REQUIRE(B < 65536 && max_blocks * page_size < (1LL << 31));
+  MK_REQUIRE(bits == 4 || bits == 8);
+  MK_REQUIRE(dtype == MK_DT_F16 || dtype == MK_DT_BF16);
+  a.q = q;
+  a.K = K_q;
+  a.V = V_q;
+  a.Ks = K_s;
+  a.Vs = V_s;
+  a.bt = block_table;
+  a.lengths = lengths;
+  a.out = out;
+  a.B = (int)B;
+  a.Hq = (int)Hq;
+  a.Hkv = (int)Hkv;
+  a.G = (int)(Hq / Hkv);
+  a.HB = (a.G + 15) / 16;
+  a.NP = (int)num_pages;
+  a.P = (int)page_size;
+  a.MB = (int)max_blocks;
+  a.gs = (int)group_size;
+  a.ngroups = (int)((D + group_size - 1) / group_size);
+  a.scale_log2 = scale * kLog2e;
+  a.vw = 1;
   return MK_OK;
 }
 
@@ -1907,34 +2042,46 @@ int mk_paged_quantized_decode_attention(const void* q, const uint8_t* K_q, const
                                         int64_t page_size, int64_t max_blocks, int64_t num_pages,
                                         int64_t group_size, int bits, float scale, int dtype,
                                         void* workspace, size_t workspace_bytes, void* stream) {
-  MK_REQUIRE(q && K_q && V_q && K_s && V_s && block_table && lengths && out);
-  MK_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && (Hq % Hkv) == 0 && D > 0 && page_size > 0);
-  MK_REQUIRE(max_blocks > 0 && num_pages > 0 && num_pages < (1LL << 31) && group_size > 0);
-  MK_REQUIRE(B < 65536 && max_blocks * page_size < (1LL << 31));
-  MK_REQUIRE(bits == 4 || bits == 8);
-  MK_REQUIRE(dtype == MK_DT_F16 || dtype == MK_DT_BF16);
-  if (B == 0) return MK_OK;
   PagedArgs a = {};
-  a.q = q;
-  a.K = K_q;
-  a.V = V_q;
-  a.Ks = K_s;
-  a.Vs = V_s;
-  a.bt = block_table;
-  a.lengths = lengths;
-  a.out = out;
+  const int rc = quant_args(a, q, K_q, V_q, K_s, V_s, block_table, lengths, out, B, Hq, Hkv, D, page_size,
+                            max_blocks, num_pages, group_size, bits, scale, dtype);
+  if (rc != MK_OK || B == 0) return rc;
   a.ws = reinterpret_cast<float*>(workspace);
-  a.B = (int)B;
-  a.Hq = (int)Hq;
-  a.Hkv = (int)Hkv;
-  a.G = (int)(Hq / Hkv);
-  a.HB = (a.G + 15) / 16;
-  a.NP = (int)num_pages;
-  a.P = (int)page_size;
-  a.MB = (int)max_blocks;
-  a.gs = (int)group_size;
-  a.ngroups = (int)((D + group_size - 1) / group_size);
-  a.scale_log2 = scale * kLog2e;
+  return attention_launch(a, D, bits, dtype, workspace_bytes,
+                          reinterpret_cast<hipStream_t>(stream));
+}
+
+int mk_paged_verify_attention(const void* q, const void* K_pages, const void* V_pages,
+                              const int32_t* block_table, const int32_t* lengths, void* out,
+                              int64_t B, int64_t W, int64_t Hq, int64_t Hkv, int64_t D, int64_t page_size,
+                              int64_t max_blocks, int64_t num_pages, float scale, int dtype,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  MK_REQUIRE(W >= 1 && W <= 64 && Hq > 0 && W * Hq < (int64_t(1) << 24) && B * W * Hq < (int64_t(1) << 31));
+  PagedArgs a = {};
+  const int rc = fp16_args(a, q, K_pages, V_pages, block_table, lengths, out, B, W * Hq, Hkv, D, page_size,
+                           max_blocks, num_pages, scale, dtype);
+  if (rc != MK_OK || B == 0) return rc;
+  a.vw = (int)W;  // W * Hq virtual heads, see PagedArgs::vw
+  a.vw_magic = (int)((65536 + W - 1) / W);
+  a.ws = reinterpret_cast<float*>(workspace);
+  return attention_launch(a, D, 0, dtype, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mk_paged_quantized_verify_attention(const void* q, const uint8_t* K_q, const uint8_t* V_q,
+                                        const f16_storage_t* K_s, const f16_storage_t* V_s,
+                                        const int32_t* block_table, const int32_t* lengths, void* out,
+                                        int64_t B, int64_t W, int64_t Hq, int64_t Hkv, int64_t D,
+                                        int64_t page_size, int64_t max_blocks, int64_t num_pages,
+                                        int64_t group_size, int bits, float scale, int dtype,
+                                        void* workspace, size_t workspace_bytes, void* stream) {
+  MK_REQUIRE(W >= 1 && W <= 64 && Hq > 0 && W * Hq < (int64_t(1) << 24) && B * W * Hq < (int64_t(1) << 31));
+  PagedArgs a = {};
+  const int rc = quant_args(a, q, K_q, V_q, K_s, V_s, block_table, lengths, out, B, W * Hq, Hkv, D, page_size,
+                            max_blocks, num_pages, group_size, bits, scale, dtype);
+  if (rc != MK_OK || B == 0) return rc;
+  a.vw = (int)W;
+  a.vw_magic = (int)((65536 + W - 1) / W);
+  a.ws = reinterpret_cast<float*>(workspace);
   return attention_launch(a, D, bits, dtype, workspace_bytes,
                           reinterpret_cast<hipStream_t>(stream));
 }

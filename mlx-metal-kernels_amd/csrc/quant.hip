@@ -197,7 +197,7 @@ int quantize_weight_launch(const void* w, uint8_t* codes, void* scales, int64_t 
 
 extern "C" {
 
-int mk_abi_version(void) { return 1; }
+int mk_abi_version(void) { return 2; }
 
 int mk_pack_q4(const uint8_t* q, uint8_t* packed, int64_t rows, int64_t K, void* stream) {
   MK_REQUIRE(q && packed && rows >= 0 && K >= 0);

@@ -74,6 +74,8 @@ SIGNATURES: dict[str, list] = {
     "mk_paged_decode_attention": [_P] * 6 + [_I64] * 7 + [_F, _I, _P, _SZ, _P],
     "mk_paged_decode_attention_noalloc": [_P] * 6 + [_I64] * 7 + [_F, _I, _P],
     "mk_paged_quantized_decode_attention": [_P] * 8 + [_I64] * 8 + [_I, _F, _I, _P, _SZ, _P],
+    "mk_paged_verify_attention": [_P] * 6 + [_I64] * 8 + [_F, _I, _P, _SZ, _P],
+    "mk_paged_quantized_verify_attention": [_P] * 8 + [_I64] * 9 + [_I, _F, _I, _P, _SZ, _P],
 }
 _RESTYPES = {"mk_paged_attention_workspace_bytes": _SZ}
 
@@ -86,7 +88,7 @@ class NativeLibraryError(RuntimeError):
 
 
 # mk_abi_version() of the library these signatures describe
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 def library_path() -> Path:

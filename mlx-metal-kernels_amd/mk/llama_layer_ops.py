@@ -208,14 +208,16 @@ def _check_decode(x, config: LlamaLikeConfig, cache, cache_layout: str):
 
 
 def llama_layer_decode_step(x, weights: LlamaLayerKernelWeights, cache, cos, sin, position, config,
-                            *, cache_layout: str = "contiguous", return_intermediates: bool = False, lengths=None):
+                            *, cache_layout: str = "contiguous", return_intermediates: bool = False, lengths=None,
+                            verify_width: int = 1):
     """ops/llama_layer_ops.py:234-428, all stages on HIP.  x [B,1,hidden];
     cache (K_pages, V_pages, block_table) for cache_layout="paged" or
     (K_cache, V_cache) [B,MAX_S,Hkv,D] for "contiguous", updated in place;
     position int or per-sequence [B].  Returns (out, cache) or
     (out, cache, intermediates).  The input RMSNorm runs inside the qkv
     matvec and the residual add inside the o-proj matvec; ``lengths``
-    (extension) = position + 1 as a device tensor shared by all layers."""
+    (extension) = position + 1 as a device tensor shared by all layers;
+    ``verify_width`` (extension): see paged_quantized_decode_block."""
     config = config.validate()
     weights.validate(config)
     K_pages, V_pages, block_table, restore = _check_decode(x, config, cache, cache_layout)
@@ -226,7 +228,8 @@ def llama_layer_decode_step(x, weights: LlamaLayerKernelWeights, cache, cos, sin
         sin, position, qkv_zeros=weights.qkv_zeros, out_zeros=weights.o_zeros, bits=weights.bits,
         group_size=weights.group_size, H=config.num_attention_heads, num_key_value_heads=config.num_key_value_heads,
         head_dim=config.head_dim, return_intermediates=return_intermediates, residual=x,
-        norm_weight=weights.input_layernorm_weight, eps=config.rms_norm_eps, lengths=lengths)
+        norm_weight=weights.input_layernorm_weight, eps=config.rms_norm_eps, lengths=lengths,
+        verify_width=verify_width)
     h, K_pages, V_pages = blk[:3]
     qkv, attn_out = (blk[3], blk[4]) if return_intermediates else (None, None)
     res = quantized_mlp_block(h, _zero_residual(h), weights.post_attention_layernorm_weight, weights.gate_w,

@@ -156,26 +156,34 @@ def greedy_sample(logits):
 
 def llama_stack_decode_step(x, stack_weights: LlamaStackWeights, stack_cache: LlamaStackCache, cos, sin, position,
                             config: LlamaLikeConfig, *, return_intermediates: bool = False, reference: bool = False,
-                            float_logits: bool = True):
+                            float_logits: bool = True, verify_width: int = 1):
     """ops/llama_stack_ops.py:352-411 on paged caches.  Returns (logits,
     final_hidden, cache) when the weights carry an lm_head, else
     (final_hidden, cache); with return_intermediates the per-layer hidden
     states are appended as a dict.  Logits are fp32; ``float_logits=False``
     keeps a quantized head's logits in the activation dtype (the widening is
-    exact, so an argmax over either agrees)."""
+    exact, so an argmax over either agrees).  ``verify_width`` W > 1
+    (extension): the rows are W draft rows per sequence (row b * W + w at
+    position[b * W + w], consecutive positions, block tables repeated W
+    times), whose attention runs as one verify launch per layer."""
     config = config.validate()
     hidden = x
     layers_out = []
     new_caches = []
     # every layer attends over positions 0..position: the lengths are shared
     lengths = position.to(torch.int32) + 1 if isinstance(position, torch.Tensor) and position.is_cuda else None
+    if verify_width > 1:
+        if lengths is None:
+            raise ValueError("verify_width needs per-row positions as a device tensor")
+        lengths = lengths[verify_width - 1::verify_width].contiguous()  # per sequence: the last row's + 1
     for li, lw in enumerate(stack_weights.layers):
         if reference:
             hidden, cache = reference_llama_layer_decode_step(hidden, lw, stack_cache.layer_caches[li], cos, sin,
                                                               position, config, cache_layout=stack_cache.cache_layout)
         else:
             hidden, cache = llama_layer_decode_step(hidden, lw, stack_cache.layer_caches[li], cos, sin, position,
-                                                    config, cache_layout=stack_cache.cache_layout, lengths=lengths)
+                                                    config, cache_layout=stack_cache.cache_layout, lengths=lengths,
+                                                    verify_width=verify_width)
         new_caches.append(cache)
         if return_intermediates:
             layers_out.append(hidden)

@@ -229,7 +229,7 @@ def paged_quantized_decode_block(x, qkv_w, qkv_scales, out_w, out_scales, K_page
                                  position, *, qkv_zeros=None, out_zeros=None, bits=4, group_size=32, H=None,
                                  num_key_value_heads=None, head_dim=None, D=None, scale=None,
                                  matvec_backend="metal_parallel", block_backend="auto", return_intermediates=False,
-                                 residual=None, norm_weight=None, eps=1e-5, lengths=None):
+                                 residual=None, norm_weight=None, eps=1e-5, lengths=None, verify_width=1):
     """ops/quantized_decode_block_ops.py:446-552: returns (projected [B,1,H*D
     -> hidden], K_pages, V_pages) or with (qkv, attn_out) appended.
 
@@ -239,7 +239,12 @@ def paged_quantized_decode_block(x, qkv_w, qkv_scales, out_w, out_scales, K_page
     ops/llama_layer_ops.py:355-359); ``norm_weight`` takes x before the
     layer's input RMSNorm and runs the norm inside the qkv matvec
     (ops/llama_layer_ops.py:256-260); ``lengths`` = position + 1 as a device
-    tensor, computed once for all layers."""
+    tensor, computed once for all layers.  ``verify_width`` W > 1: x holds W
+    consecutive draft rows per sequence (row b * W + w at position
+    position[b * W + w], the block table repeated W times); the attention
+    then runs as mk_paged_verify_attention over the sequences' own table rows
+    (one K/V read for the W rows), with ``lengths`` (required) per sequence,
+    the last row's position + 1."""
     x2d, _, _ = normalize_hidden_input(x)
     H, kv_heads, D = _block_dims(qkv_w, H, num_key_value_heads, head_dim, D, bits)
     validate_quantized_weight_shapes(x2d, qkv_w, qkv_scales, qkv_zeros, bits=bits, group_size=group_size,
@@ -258,8 +263,18 @@ def paged_quantized_decode_block(x, qkv_w, qkv_scales, out_w, out_scales, K_page
             num_attention_heads=H, num_key_value_heads=kv_heads, head_dim=D, bits=bits, group_size=group_size,
             eps=eps)
         sc = 1.0 / math.sqrt(D) if scale is None else scale
-        attn_out = _hip_paged_attention(q[:, 0], K_pages, V_pages, _i32(block_table, q.device),
-                                        pos + 1 if lengths is None else lengths, sc).unsqueeze(1)
+        if verify_width > 1:
+            from .speculative_verify_ops import _hip_verify_attention
+
+            W = verify_width
+            if lengths is None or q.shape[0] % W:
+                raise ValueError("verify_width needs B * W rows and per-sequence lengths")
+            bt_seq = block_table[::W].contiguous()
+            attn_out = _hip_verify_attention(q.reshape(-1, W, H, D), K_pages, V_pages, bt_seq, lengths,
+                                             sc).reshape(q.shape[0], 1, H, D)
+        else:
+            attn_out = _hip_paged_attention(q[:, 0], K_pages, V_pages, _i32(block_table, q.device),
+                                            pos + 1 if lengths is None else lengths, sc).unsqueeze(1)
     elif norm_weight is not None and not reference:
         qkv = q_rmsnorm_matvec(x2d, norm_weight, qkv_w, qkv_scales, qkv_zeros, bits=bits, group_size=group_size,
                                eps=eps).reshape(x2d.shape[0], 1, -1)
@@ -278,7 +293,8 @@ def paged_quantized_decode_block(x, qkv_w, qkv_scales, out_w, out_scales, K_page
     else:
         attn_out, K_pages, V_pages = paged_gqa_decode_block_from_qkv(
             qkv, K_pages, V_pages, block_table, cos, sin, position, num_attention_heads=H,
-            num_key_value_heads=kv_heads, head_dim=D, scale=scale, backend=block_backend, lengths=lengths)
+            num_key_value_heads=kv_heads, head_dim=D, scale=scale, backend=block_backend,
+            lengths=lengths if verify_width == 1 else None)  # verify rows here: one sequence each
     B = attn_out.shape[0]
     a2d = attn_out.reshape(B, H * D)
     if residual is not None and not reference:

@@ -7,9 +7,11 @@ position ``position + i`` on a cloned cache, each attending over the context
 plus the drafts before it.  Here the K drafts run through the stack as K rows
 of one pass: every projection is a K-row matvec (one read of each weight
 matrix instead of K), every layer's fused front writes the K new K/V rows,
-and the paged attention then runs the K rows as K sequences that share the
-block-table row, row i with length ``position + i + 1`` -- the same causal
-structure in one attention launch per layer.
+and the verify attention kernel (``mk_paged_verify_attention``) then serves
+all K rows of a sequence from one read of its K/V: the K * Hq/Hkv query rows
+of a kv head are the columns of one MFMA contraction, row i masked at
+position ``position + i + 1`` -- the same causal structure in one attention
+launch per layer.
 
 Config, result, acceptance and commit helpers keep the reference's names,
 fields and errors; ``cache_layout`` accepts "paged" as well as the
@@ -32,8 +34,8 @@ from .llama_layer_ops import LlamaLikeConfig
 from .llama_stack_ops import (LlamaStackCache, LlamaStackWeights, embed_token_ids, greedy_sample,
                               llama_stack_decode_step)
 from . import _contig
-from .paged_kv_ops import _hip_paged_attention
-from .paged_quantized_kv_ops import PagedQuantizedKVCache, _hip_quantized_attention, dequantize_kv_pages
+from .paged_kv_ops import _i32
+from .paged_quantized_kv_ops import PagedQuantizedKVCache, _check_kernel_layout, dequantize_kv_pages
 
 _ACT = (torch.float16, torch.bfloat16)
 
@@ -218,22 +220,34 @@ def reference_paged_verify_attention(q, K_pages, V_pages, block_table, lengths=N
     return torch.cat(rows, dim=1)
 
 
-def _row_tables(block_table, ln, W):
-    """The verify rows as sequences of their own: block table rows repeated
-    W times, row w of sequence b with length lengths[b] - (W - 1 - w) (>= 0)."""
-    rows_bt = block_table.repeat_interleave(W, dim=0)
-    off = torch.arange(W - 1, -1, -1, dtype=torch.int32, device=ln.device)
-    rows_len = torch.clamp(ln.to(torch.int32)[:, None] - off[None, :], min=0).reshape(-1)
-    return rows_bt, rows_len
+def _hip_verify_attention(q, K_pages, V_pages, block_table, ln, scale: float):
+    """mk_paged_verify_attention: q [B,W,Hq,D] over fp16/bf16 pages, one K/V
+    read for all W rows of a sequence."""
+    B, W, Hq, D = q.shape
+    NUM_PAGES, P, Hkv, _ = K_pages.shape
+    MAX_BLOCKS = block_table.shape[1]
+    dev = _lib.require_device(q, K_pages, V_pages, block_table)
+    dtype = K_pages.dtype
+    if V_pages.dtype != dtype:
+        raise TypeError(f"K_pages and V_pages must share a dtype, got {dtype}, {V_pages.dtype}")
+    qc = q.to(dtype).contiguous()
+    Kp, Vp = K_pages.contiguous(), V_pages.contiguous()
+    bt, lnd = _i32(block_table, dev), _i32(ln, dev)
+    out = torch.empty((B, W, Hq, D), dtype=dtype, device=dev)
+    ws, ws_bytes = _lib.attention_workspace(dev, B, W * Hq, Hkv, D, MAX_BLOCKS, P)
+    _lib.launch("mk_paged_verify_attention", dev, _lib.ptr(qc), _lib.ptr(Kp), _lib.ptr(Vp), _lib.ptr(bt),
+                _lib.ptr(lnd), _lib.ptr(out), B, W, Hq, Hkv, D, P, MAX_BLOCKS, NUM_PAGES, float(scale),
+                _lib.dtype_code(dtype), _lib.ptr(ws), ws_bytes)
+    return out
 
 
 def paged_verify_attention(q, K_pages, V_pages, block_table, lengths=None, scale=None, *, backend: str = "auto"):
     """W causal query rows per sequence over an fp16/bf16 paged cache in one
     HIP launch.  q [B,W,Hq,D]; K/V_pages [NUM_PAGES,P,Hkv,D]; lengths [B]
     count the context and all W new positions (already written); row w sees
-    positions < lengths[b] - (W-1-w), none -> zeros.  The rows run as B*W
-    sequences of the paged decode kernel sharing their sequence's block-table
-    row.  backend 'reference' runs reference_paged_verify_attention."""
+    positions < lengths[b] - (W-1-w), none -> zeros.  Each K/V byte is read
+    once for the W rows (mk_paged_verify_attention).  backend 'reference'
+    runs reference_paged_verify_attention."""
     max_s = block_table.shape[1] * K_pages.shape[1]
     B, W, ln = _verify_shapes(q, block_table, lengths, max_s)
     if backend.lower() == "reference":
@@ -245,10 +259,7 @@ def paged_verify_attention(q, K_pages, V_pages, block_table, lengths=None, scale
     if q.shape[3] != K_pages.shape[3] or q.shape[2] % K_pages.shape[2]:
         raise ValueError(f"q {tuple(q.shape)} does not fit pages {tuple(K_pages.shape)}")
     sc = 1.0 / math.sqrt(q.shape[3]) if scale is None else scale
-    rows_bt, rows_len = _row_tables(block_table, torch.clamp(ln, max=max_s), W)
-    B, W, Hq, D = q.shape
-    out = _hip_paged_attention(q.reshape(B * W, Hq, D), K_pages, V_pages, rows_bt, rows_len, sc)
-    return out.reshape(B, W, Hq, D).to(q.dtype)
+    return _hip_verify_attention(q, K_pages, V_pages, block_table, ln, sc).to(q.dtype)
 
 
 def paged_quantized_verify_attention(q, paged_qkv: PagedQuantizedKVCache, lengths=None, scale=None, *,
@@ -264,13 +275,24 @@ def paged_quantized_verify_attention(q, paged_qkv: PagedQuantizedKVCache, length
         return reference_paged_verify_attention(q, Kp.to(q.dtype), Vp.to(q.dtype), paged_qkv.block_table, ln, sc)
     if backend.lower() not in ("auto", "metal"):
         raise ValueError("backend must be one of 'reference', 'metal', 'auto'")
-    import dataclasses
-
-    rows_bt, rows_len = _row_tables(paged_qkv.block_table, torch.clamp(ln, max=max_s), W)
-    rows = dataclasses.replace(paged_qkv, block_table=rows_bt, lengths=rows_len)
     Bq, Wq, Hq, D = q.shape
-    out = _hip_quantized_attention(q.reshape(Bq * Wq, 1, Hq, D), rows, rows_len, sc)
-    return out.reshape(Bq, Wq, Hq, D)
+    _, _, Hkv, _ = paged_qkv.original_page_shape
+    P = int(paged_qkv.page_size)
+    NUM_PAGES = _check_kernel_layout(paged_qkv, Hkv, D)
+    kq, vq = paged_qkv.k_pages_q.contiguous(), paged_qkv.v_pages_q.contiguous()
+    ks = paged_qkv.k_scales.to(torch.float16).contiguous()
+    vs = paged_qkv.v_scales.to(torch.float16).contiguous()
+    dev = _lib.require_device(q, kq, vq, ks, vs)
+    qc = q.contiguous()
+    bt, lnd = _i32(paged_qkv.block_table, dev), _i32(ln, dev)
+    MAX_BLOCKS = bt.shape[1]
+    out = torch.empty((Bq, Wq, Hq, D), dtype=q.dtype, device=dev)
+    ws, ws_bytes = _lib.attention_workspace(dev, Bq, Wq * Hq, Hkv, D, MAX_BLOCKS, P)
+    _lib.launch("mk_paged_quantized_verify_attention", dev, _lib.ptr(qc), _lib.ptr(kq), _lib.ptr(vq),
+                _lib.ptr(ks), _lib.ptr(vs), _lib.ptr(bt), _lib.ptr(lnd), _lib.ptr(out), Bq, Wq, Hq, Hkv, D, P,
+                MAX_BLOCKS, NUM_PAGES, paged_qkv.group_size, paged_qkv.bits, float(sc), _lib.dtype_code(q.dtype),
+                _lib.ptr(ws), ws_bytes)
+    return out
 
 
 # ------------------------------------------------------------ one verify pass
@@ -279,8 +301,11 @@ def paged_quantized_verify_attention(q, paged_qkv: PagedQuantizedKVCache, length
 def _rows_cache(stack_cache: LlamaStackCache, B: int, W: int) -> LlamaStackCache:
     """The stack cache as seen by B*W verify rows: the same K/V pages (a
     contiguous cache through its identity-paged view), each sequence's
-    block-table row repeated W times."""
+    block-table row repeated W times (for the rows' cache writes; the
+    attention takes every W-th row back).  Layers that share a block table
+    share its repetition."""
     layers = []
+    repeated: dict = {}
     for lc in stack_cache.layer_caches:
         if stack_cache.cache_layout == "paged":
             K, V, bt = lc
@@ -292,7 +317,10 @@ def _rows_cache(stack_cache: LlamaStackCache, B: int, W: int) -> LlamaStackCache
             bt = _contig.identity_table(Kc.shape[0], S, P, Kc.device)
         if bt.shape[0] != B:
             raise ValueError(f"the cache holds {bt.shape[0]} sequences, x has {B}")
-        layers.append((K, V, bt.repeat_interleave(W, dim=0)))
+        key = (bt.data_ptr(), tuple(bt.shape))
+        if key not in repeated:
+            repeated[key] = bt.repeat_interleave(W, dim=0)
+        layers.append((K, V, repeated[key]))
     P = layers[0][0].shape[1] if layers else stack_cache.page_size
     return LlamaStackCache(layers, "paged", stack_cache.max_seq_len, P)
 
@@ -314,7 +342,7 @@ def llama_stack_verify_step(x, stack_weights: LlamaStackWeights, stack_cache: Ll
     p0 = normalize_positions(position, B, stack_cache.max_seq_len - W + 1, device=dev).to(torch.int32)
     pos_rows = (p0[:, None] + torch.arange(W, dtype=torch.int32, device=dev)[None, :]).reshape(B * W)
     res = llama_stack_decode_step(x.reshape(B * W, 1, H), stack_weights, _rows_cache(stack_cache, B, W), cos, sin,
-                                  pos_rows, config, float_logits=float_logits)
+                                  pos_rows, config, float_logits=float_logits, verify_width=W)
     if stack_weights.lm_head is None:
         fh, _ = res
         return None, fh.reshape(B, W, H), stack_cache

@@ -1,9 +1,10 @@
 """Multi-row (speculative-verify) paged attention and the one-pass verify of
-a draft: the HIP path (W rows as sequences of the paged decode kernel sharing
-the block-table row) against oracle.paged_verify_attention (the staged decode
-loop of ops/speculative_verify_ops.py:228-262 restated), the stack-level pass
-against W staged HIP decode steps and the oracle, and the accept /
-replacement / commit rules."""
+a draft: the HIP path (mk_paged_verify_attention: the W * Hq/Hkv rows of a kv
+head as the columns of one MFMA contraction over one K/V read, row w masked
+at its own causal limit) against oracle.paged_verify_attention (the staged
+decode loop of ops/speculative_verify_ops.py:228-262 restated), the
+stack-level pass against W staged HIP decode steps and the oracle, and the
+accept / replacement / commit rules."""
 
 import numpy as np
 import pytest
@@ -79,6 +80,29 @@ def test_verify_attention_config3_lengths(dev, W):
                                     _t(lengths, dev, torch.int32))
     ref = op.paged_verify_attention(q, K16, V16, bt, lengths)
     assert_close(got, ref, what=f"config-3 verify W={W}")
+
+
+@pytest.mark.parametrize("B,W,Hq,Hkv,mb", [(2, 4, 32, 8, 8), (2, 3, 24, 3, 6), (16, 4, 32, 8, 512), (16, 5, 40, 5, 512)])
+def test_verify_causal_limits_straddle_blocks(dev, B, W, Hq, Hkv, mb):
+    """Lengths 32k + 1 .. 32k + W - 2, so the W rows' limits fall on both
+    sides of a 32-position block boundary (and, for the long tables, of
+    split boundaries of the stream plan); W * G columns that are not a
+    multiple of 16 (G = 8, W = 3 / 5) put a row boundary inside a 16-column
+    tile.  Short tables run the short-context plan, 8192-wide tables the
+    stream plan."""
+    print(f"verify limits B={B} W={W} Hq={Hq} Hkv={Hkv} mb={mb}", flush=True)
+    rng = np.random.default_rng(B * 100 + W * 10 + Hq)
+    D, P = 128, 16
+    K, V, bt = _pages(rng, B, mb, P, Hkv, D)
+    K16, V16 = K.astype(np.float16), V.astype(np.float16)
+    q = rng.standard_normal((B, W, Hq, D)).astype(np.float16)
+    k = rng.integers(1, (mb * P) // 32, size=B)
+    lengths = 32 * k + 1 + (np.arange(B) % max(1, W - 2))
+    got = sv.paged_verify_attention(_t(q, dev, torch.float16), _t(K16, dev, torch.float16),
+                                    _t(V16, dev, torch.float16), _t(bt, dev, torch.int32),
+                                    _t(lengths, dev, torch.int32))
+    ref = op.paged_verify_attention(q, K16, V16, bt, lengths)
+    assert_close(got, ref, what=f"verify limits B={B} W={W}")
 
 
 def test_verify_width_one_is_decode_bit_exact(dev):

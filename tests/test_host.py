@@ -66,7 +66,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_workspace():
     lib = _lib.load()
-    assert lib.mk_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.mk_abi_version() == _lib.ABI_VERSION == 2
     # split-KV partials: B*Hq*splits*(D+2) fp32, never 0 for a real shape
     ws = _lib.workspace_bytes(16, 32, 8, 128, 512, 16)
     assert ws > 0 and ws % 4 == 0

@@ -78,12 +78,20 @@ def test_reference_verify_attention_matches_oracle(W):
     assert_close(got, op.paged_verify_attention(q, Kp, Vp, bt, lengths), what=f"reference verify W={W}")
 
 
-def test_row_tables():
+def test_rows_cache_repeats_tables_once():
+    """The stack verify pass writes row b * W + w through table row b
+    (repeated W times); layers that share a block table share one
+    repetition."""
+    from mk.llama_stack_ops import LlamaStackCache
+
     bt = torch.tensor([[3, 4], [7, 8]], dtype=torch.int32)
-    rows_bt, rows_len = sv._row_tables(bt, torch.tensor([10, 2], dtype=torch.int32), 3)
-    assert rows_bt.tolist() == [[3, 4]] * 3 + [[7, 8]] * 3
-    assert rows_len.tolist() == [8, 9, 10, 0, 1, 2]
-    assert np.array_equal(rows_len.numpy().reshape(2, 3), op.verify_row_lengths([10, 2], 3))
+    K = torch.zeros(9, 4, 2, 8, dtype=torch.float16)
+    cache = LlamaStackCache([(K, K, bt), (K, K, bt)], "paged", 8, 4)
+    rows = sv._rows_cache(cache, 2, 3)
+    (_, _, r0), (_, _, r1) = rows.layer_caches
+    assert r0.tolist() == [[3, 4]] * 3 + [[7, 8]] * 3
+    assert r1 is r0
+    assert np.array_equal(r0.numpy()[::3], bt.numpy())  # the attention's per-sequence rows
 
 
 def test_hip_verify_path_needs_a_device():
