@@ -64,6 +64,9 @@ def _parse():
                          "attention), attn_short (fp16 attention at B=1 2k / 8k and B=4 2k), config4 (q8/q4 KV "
                          "attention), mlp_m4 / mlp_m8 / mlp_m32 (batched q4 MLP "
                          "steps), mlp_q8 (q8 MLP step, M=1), stack (config-5 decode stack)")
+    ap.add_argument("--cases", default=None,
+                    help="with --workload verify: comma-separated widths (default 2,4,8); with --workload "
+                         "attn_short: comma-separated case names (B1_ctx2048, B1_ctx8192, B4_ctx2048)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="first run a plain device copy of this many MiB (counter calibration)")
     ap.add_argument("--summarize-counters", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -258,7 +261,7 @@ def attention_config3(dev, steps, warmup):
     }
 
 
-def attention_short(dev, steps=200, warmup=20):
+def attention_short(dev, steps=200, warmup=20, cases=None):
     """Short total contexts (the one-kernel short-context plan): one sequence
     of 2048 and of 8192 positions, and four of ~2k -- Hq 32 / Hkv 8, D=128,
     P=16, fp16 K/V ~ N(0,1), a seeded permuted block table as wide as the
@@ -273,6 +276,8 @@ def attention_short(dev, steps=200, warmup=20):
     Hq, Hkv, D, P = 32, 8, 128, 16
     out = {}
     for name, lengths in (("B1_ctx2048", [2048]), ("B1_ctx8192", [8192]), ("B4_ctx2048", [2048, 2049, 2100, 2176])):
+        if cases and name not in cases:
+            continue
         B = len(lengths)
         mb = -(-max(lengths) // P)
         NP = B * mb
@@ -740,9 +745,11 @@ def run_workload(name, dev, args):
     if name == "config4":
         return attention_config4(dev)
     if name == "verify":
-        return attention_verify(dev)
+        widths = tuple(int(w) for w in args.cases.split(",")) if args.cases else (2, 4, 8)
+        return attention_verify(dev, widths=widths)
     if name == "attn_short":
-        return {"workload": "paged_gqa_fp16_short_contexts", **attention_short(dev)}
+        cases = args.cases.split(",") if args.cases else None
+        return {"workload": "paged_gqa_fp16_short_contexts", **attention_short(dev, cases=cases)}
     if name == "stack":
         return decode_stack_config5(dev)
     sets = [make_mlp_set(dev, 4, 100 + i) for i in range(args.sets)]
