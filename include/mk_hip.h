@@ -43,7 +43,7 @@ extern "C" {
 /* IEEE binary16 value held as its raw bits (quantized-KV scales). */
 typedef uint16_t f16_storage_t;
 
-/* ABI version; bumped on any signature change. */
+/* ABI version; bumped when entry points are added or their signatures change. */
 int mk_abi_version(void);
 
 /* ---------------------------------------------------------------- q4/q8 pack / dequant */
