@@ -5,6 +5,7 @@ TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
 
 from __future__ import annotations
 
+import contextlib
 import math
 
 import numpy as np
@@ -69,7 +70,7 @@ def matvec(x: np.ndarray, W_deq: np.ndarray, act: str = "f16") -> np.ndarray:
     """ops/quant_ops.py:509-526: fp32 matmul of x with W already rounded to
     x's dtype, clipped to the finite range of x's dtype, cast to it.
     act="bf16" returns bf16 values held in fp32."""
-    y = x.astype(np.float32) @ W_deq.astype(np.float32).T
+    y = x.astype(np.float32) @ np.asarray(W_deq, dtype=np.float32).T
     m = F16_MAX if act == "f16" else BF16_MAX
     return _cast(np.clip(y, -m, m), act)
 
@@ -79,15 +80,45 @@ def _deq_act(codes_unpacked, scales, zeros, group_size, act):
     return w.astype(np.float16) if act == "f16" else round_bf16(w)
 
 
+# Dequantized weights of q4_matvec / q8_matvec, reused while a
+# memoized_dequant() block is open: keyed by the identity of the code, scale
+# and zero arrays (held by the memo, so the keys stay unique), for tests that
+# run one weight set many times (a deep stack whose layers share weights).
+_DEQ_MEMO = None
+
+
+@contextlib.contextmanager
+def memoized_dequant():
+    global _DEQ_MEMO
+    _DEQ_MEMO = {}
+    try:
+        yield
+    finally:
+        _DEQ_MEMO = None
+
+
+def _deq_cached(make, arrays, key):
+    if _DEQ_MEMO is None:
+        return make()
+    k = tuple(id(a) for a in arrays) + key
+    if k not in _DEQ_MEMO:
+        _DEQ_MEMO[k] = (make().astype(np.float32), arrays)
+    return _DEQ_MEMO[k][0]
+
+
 def q4_matvec(x, packed, scales, zeros=None, group_size=32, act="f16"):
     """ops/quant_ops.py:509-526 (W rounded to the activation dtype)."""
     K = x.shape[1]
-    return matvec(x, _deq_act(unpack_q4(packed, K), scales, zeros, group_size, act), act)
+    W = _deq_cached(lambda: _deq_act(unpack_q4(packed, K), scales, zeros, group_size, act), (packed, scales, zeros),
+                    ("q4", K, group_size, act))
+    return matvec(x, W, act)
 
 
 def q8_matvec(x, q, scales, zeros=None, group_size=32, act="f16"):
     """ops/quant_ops.py:574-588."""
-    return matvec(x, _deq_act(np.asarray(q, dtype=np.uint8), scales, zeros, group_size, act), act)
+    W = _deq_cached(lambda: _deq_act(np.asarray(q, dtype=np.uint8), scales, zeros, group_size, act), (q, scales, zeros),
+                    ("q8", group_size, act))
+    return matvec(x, W, act)
 
 
 def q4_matvec_w32(x, packed, scales, zeros=None, group_size=32, act="f16"):

@@ -1,7 +1,9 @@
 """Config 5 at its real shape: Llama-3-8B layer geometry (hidden 4096, 32/8
 heads, head_dim 128, intermediate 14336, q4 group 64, paged fp16 KV, P 16,
 RoPE theta 500000) against the oracle, at batch 1 and 32, plus one stack step
-through the 128256-entry q4 head and the HIP row argmax.
+through the 128256-entry q4 head and the HIP row argmax, and the benched
+32-layer stack: one step held layer by layer against the oracle, and the
+graph-replayed decode loop against eager steps.
 
 Weights are random codes (uniform 0..15, zero point 8) with fp16 scales in
 [0.002, 0.004] -- the statistics of N(0, 0.02) weights quantized at group 64 --
@@ -195,3 +197,134 @@ def test_head_full_shape_batched(dev, B):
     got = y.float().cpu().numpy()[:, rows]
     ref = oq.q4_matvec(nrm, hc[rows], hs[rows], hz[rows], group_size=G)
     assert_close(got, ref, what=f"head rows B={B}")
+
+
+# ------------------------------------------------------------ full depth
+
+LAYERS = 32
+
+
+def _deep_stack(dev, seed, B):
+    """32 Llama-3-8B-shape layers sharing one random q4 weight set (so the
+    oracle dequantizes it once), the 128256-entry q4 head, and the embedding
+    table and per-layer paged caches of ~2048 positions drawn on the device.
+    Returns the embedding rows of the tokens (host) for the oracle.
+
+    The o-proj and down scales are a tenth of the others: with one weight set
+    in every layer the layers' residual updates line up, and at full size the
+    stream would grow outliers whose fp16 ulps exceed the tolerance; at a
+    tenth each layer adds ~0.1 and the stream keeps its N(0, 1) scale over 32
+    layers, as in the one-layer tests."""
+    rng = np.random.default_rng(seed)
+    cfg = _cfg(LAYERS, VOCAB)
+    lw = _np_layer(rng)
+    for name in ("o", "down"):
+        c, sc, z = lw[name]
+        lw[name] = (c, (sc * 0.1).astype(np.float16).astype(np.float32), z)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    emb_t = torch.randn((VOCAB, H), device=dev, generator=gen).to(torch.float16)
+    head = _q4(rng, VOCAB, H)
+    fnorm = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float16)
+    tw = _t_layer(lw, dev, 4, G)
+    hc, hs, hz = head
+    wts = ls.LlamaStackWeights(
+        layers=[tw] * LAYERS, final_norm_weight=torch.from_numpy(fnorm).to(dev),
+        lm_head=ls.QuantizedHead(torch.from_numpy(hc).to(dev), torch.from_numpy(hs).to(torch.float16).to(dev),
+                                 torch.from_numpy(hz).to(torch.float16).to(dev), 4, G),
+        embedding=emb_t).validate(cfg)
+    mb = CTX // P + 4
+    NP = B * mb + 2
+    bt = rng.permutation(NP)[:B * mb].astype(np.int32).reshape(B, mb)
+    caches = [(torch.randn((NP, P, HKV, D), device=dev, generator=gen).to(torch.float16),
+               torch.randn((NP, P, HKV, D), device=dev, generator=gen).to(torch.float16)) for _ in range(LAYERS)]
+    pos = rng.integers(CTX - 64, CTX, size=B).astype(np.int32)
+    tokens = rng.integers(0, VOCAB, size=B)
+    emb_rows = emb_t[torch.from_numpy(tokens).to(dev)].cpu().numpy()
+    return cfg, lw, emb_rows, head, fnorm, wts, bt, caches, pos, tokens, mb
+
+
+@pytest.mark.parametrize("B,checked", [(1, tuple(range(LAYERS))), (32, (0, 1, 16, LAYERS - 1))])
+def test_full_depth_stack_step_vs_oracle(dev, B, checked):
+    """One decode step of the benched config-5 stack -- 32 Llama-3-8B-shape
+    q4 layers, the 128256 x 4096 q4 head, ~2048-position paged caches -- at
+    batch 1 and 32.  Each checked layer is held against the oracle layer run
+    on that layer's HIP input (so the differences of earlier layers do not
+    compound): its output at the tolerance of the one-layer test, its written
+    K/V slot, every other cache row untouched.  The final norm and the head
+    are checked on the HIP final hidden state."""
+    print(f"full-depth stack B={B}", flush=True)
+    cfg, lw, emb, head, fnorm, wts, bt, caches, pos, tokens, mb = _deep_stack(dev, 1000 + B, B)
+    cos, sin = op.rope_tables(cfg.max_position_embeddings, D, cfg.rope_theta)
+    tc, ts = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+    btt = torch.from_numpy(bt).to(dev)
+    before = {li: (caches[li][0].cpu().numpy(), caches[li][1].cpu().numpy()) for li in checked}
+    cache = ls.LlamaStackCache([(K, V, btt) for K, V in caches], "paged", mb * P, P)
+    x = ls.embed_token_ids(torch.from_numpy(tokens).to(dev), wts.embedding)
+    logits, final_hidden, cache, inter = ls.llama_stack_decode_step(
+        x, wts, cache, tc, ts, torch.from_numpy(pos).to(dev), cfg, float_logits=False, return_intermediates=True)
+    torch.cuda.synchronize(dev)
+    outs = [t[:, 0].cpu().numpy() for t in inter["layers"]]
+    page, off = op.block_table_lookup(bt, pos, P)
+    with oq.memoized_dequant():
+        for li in checked:
+            xin = emb[:] if li == 0 else outs[li - 1]
+            K0, V0 = before[li]
+            ref, Kr, Vr = ol.layer_decode_step(xin, lw, K0, V0, bt, cos, sin, pos, HQ, HKV, D, 4, G)
+            assert_close(outs[li], ref, extra=2 * _ulp16(xin) + 2 * _ulp16(outs[li]), what=f"layer {li} B={B}")
+            K2, V2 = (t.cpu().numpy() for t in cache.layer_caches[li][:2])
+            for b in range(B):
+                # k and v are 4096-term projections of the normalised input,
+                # which the HIP norm and the oracle may round one ulp apart
+                # in any element: with every element off by an ulp of random
+                # sign the error's std is 2^-11 rms(k) (rms(k) = |W|_rms
+                # |n|_2), plus half that for the M = 1 kernel's fp32 W; at
+                # the residual stream of deep layers such flips are common,
+                # so allow 6 x 2^-11 rms -- about 5 sigma over B x 1024 values
+                for nm, got_kv, ref_kv in (("k", K2, Kr), ("v", V2, Vr)):
+                    r = ref_kv[page[b], off[b]].astype(np.float64)
+                    assert_close(got_kv[page[b], off[b]], r, extra=6 * 2.0 ** -11 * np.sqrt(np.mean(r * r)),
+                                 what=f"layer {li} {nm} written b{b}")
+            untouched = np.ones(K0.shape[:2], bool)
+            untouched[page, off] = False
+            assert np.array_equal(K2[untouched], K0[untouched]) and np.array_equal(V2[untouched], V0[untouched])
+            del K2, V2, K0, V0, Kr, Vr
+            before.pop(li)
+        hl = outs[-1]
+        fh = final_hidden[:, 0].float().cpu().numpy()
+        assert np.all(np.abs(fh - oq.rms_norm(hl, fnorm).astype(np.float32)) <= _ulp16(oq.rms_norm(hl, fnorm)) + 1e-7)
+        got = logits.float().cpu().numpy().reshape(B, VOCAB)
+        assert_close(got, oq.q4_matvec(final_hidden[:, 0].cpu().numpy(), *head, group_size=G), what=f"head B={B}")
+    assert np.array_equal(ls.greedy_sample(logits).cpu().numpy(), np.argmax(got, axis=-1))
+
+
+@pytest.mark.parametrize("B", [1, 32])
+def test_full_depth_decode_graph_matches_eager(dev, B):
+    """The benched config-5 loop: DecodeGraph (one eager step, then HIP graph
+    replays) against eager llama_stack_decode_step calls fed back their own
+    greedy tokens, on copies of the same 32-layer caches: tokens of every
+    step and every cache byte after three steps identical."""
+    print(f"full-depth decode graph B={B}", flush=True)
+    cfg, _, _, _, _, wts, bt, caches, pos, tokens, mb = _deep_stack(dev, 1100 + B, B)
+    cos, sin = op.rope_tables(cfg.max_position_embeddings, D, cfg.rope_theta)
+    tc, ts = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+    btt = torch.from_numpy(bt).to(dev)
+    c1 = ls.LlamaStackCache([(K.clone(), V.clone(), btt) for K, V in caches], "paged", mb * P, P)
+    c2 = ls.LlamaStackCache([(K, V, btt) for K, V in caches], "paged", mb * P, P)
+    tok = torch.from_numpy(tokens).to(dev)
+    p = torch.from_numpy(pos).to(dev)
+    graph = ls.DecodeGraph(wts, c1, tc, ts, cfg, tok, p)
+    got = [graph.first_tokens.clone(), graph.step().clone(), graph.step().clone()]
+    torch.cuda.synchronize(dev)
+    want = []
+    t, pp = tok.clone(), p.clone().to(torch.int32)
+    for _ in range(3):
+        lg, _, c2 = ls.llama_stack_decode_step(ls.embed_token_ids(t, wts.embedding), wts, c2, tc, ts, pp, cfg,
+                                               float_logits=False)
+        t = ls.greedy_sample(lg)
+        want.append(t.clone())
+        pp = pp + 1
+    for s, (a, b) in enumerate(zip(got, want)):
+        assert torch.equal(a, b), f"step {s} tokens"
+    for li, ((K1, V1, _), (K2, V2, _)) in enumerate(zip(c1.layer_caches, c2.layer_caches)):
+        assert torch.equal(K1, K2) and torch.equal(V1, V2), f"layer {li} caches"

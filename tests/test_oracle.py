@@ -539,3 +539,22 @@ def test_metal_semantics_matvec_one_hot_and_w_rounding():
     bound = (np.abs(x.astype(np.float64)) @ np.abs(W32.astype(np.float64)).T) * 2.0 ** -11
     assert np.all(np.abs(a - b) <= bound + (np.abs(a) + np.abs(b)) * 2.0 ** -11 + 1e-7)
     assert not np.array_equal(a, b)  # the two semantics are distinguishable
+
+
+def test_memoized_dequant_matches_and_reuses():
+    """oracle.quant.memoized_dequant: the same matvec results as without it,
+    one dequantization per weight array set, nothing kept after the block."""
+    rng = np.random.default_rng(92)
+    packed = rng.integers(0, 256, size=(32, 64), dtype=np.uint8)
+    s = rng.uniform(0.01, 0.02, size=(32, 4)).astype(np.float32)
+    z = np.full((32, 4), 8.0, np.float32)
+    x = rng.standard_normal((2, 128)).astype(np.float16)
+    plain = oq.q4_matvec(x, packed, s, z, 32)
+    with oq.memoized_dequant():
+        a = oq.q4_matvec(x, packed, s, z, 32)
+        b = oq.q4_matvec(x[:1], packed, s, z, 32)
+        assert len(oq._DEQ_MEMO) == 1
+        oq.q8_matvec(x, rng.integers(0, 256, size=(8, 128), dtype=np.uint8), s[:8], z[:8], 32)
+        assert len(oq._DEQ_MEMO) == 2
+    assert oq._DEQ_MEMO is None
+    assert np.array_equal(a, plain) and np.array_equal(b, plain[:1])
