@@ -18,7 +18,9 @@ carries:
                    HIP events, against the 8 TB/s HBM peak;
   cpu_baseline  -- the numpy oracle (the reference's array path restated)
                    timed on this host for a bounded sample of the same step;
-  extra         -- M=4/8/32 and q8 variants, paged GQA decode attention at
+  extra         -- the q4 GEMVs of the step on their own (gate/up + SwiGLU,
+                   down; config 1's 4096x4096 matvec), M=4/8/32 and q8
+                   variants, paged GQA decode attention at
                    BASELINE config 3 and at short contexts, config 4 (q8/q4
                    KV), the speculative-verify attention at config-3 geometry
                    (W = 2/4/8 rows, MFMA TFLOP/s beside HBM GB/s) and the
@@ -45,7 +47,7 @@ TRAFFIC_SUMMARY = "gemv_dot_q4_rmsnorm_gate_up_M1_traffic.json"
 ATTN_TRAFFIC_SUMMARY = "paged_attn_config3_fp16_traffic.json"
 
 
-WORKLOADS = ("config3", "attn_short", "config4", "verify", "mlp_m4", "mlp_m8", "mlp_m32", "mlp_q8", "stack")
+WORKLOADS = ("config3", "attn_short", "config4", "verify", "gemv", "mlp_m4", "mlp_m8", "mlp_m32", "mlp_q8", "stack")
 PEAK_MFMA_F16_TFLOPS = 2500.0  # dense fp16 MFMA peak of MI355X
 
 
@@ -62,8 +64,9 @@ def _parse():
     ap.add_argument("--workload", choices=WORKLOADS, default=None,
                     help="run one workload alone and print its JSON (for profiling): config3 (paged fp16 "
                          "attention), attn_short (fp16 attention at B=1 2k / 8k and B=4 2k), config4 (q8/q4 KV "
-                         "attention), mlp_m4 / mlp_m8 / mlp_m32 (batched q4 MLP "
-                         "steps), mlp_q8 (q8 MLP step, M=1), stack (config-5 decode stack)")
+                         "attention), gemv (config 2's q4 gate/up + SwiGLU and down GEMVs and config 1's "
+                         "matvec, M=1, without the block's norm and residual), mlp_m4 / mlp_m8 / mlp_m32 "
+                         "(batched q4 MLP steps), mlp_q8 (q8 MLP step, M=1), stack (config-5 decode stack)")
     ap.add_argument("--cases", default=None,
                     help="with --workload verify: comma-separated widths (default 2,4,8); with --workload "
                          "attn_short: comma-separated case names (B1_ctx2048, B1_ctx8192, B4_ctx2048)")
@@ -738,6 +741,45 @@ def mlp_extra(dev, sets, M, bits, steps, warmup=12):
             "frac_of_peak": bb / (m_ms * 1e-3) / 1e9 / PEAK_GBS, "bytes": bb}
 
 
+def gemv_extra(dev, sets, steps, warmup=12):
+    """Config 2's q4 GEMVs at M = 1 on their own, without the MLP block's
+    residual + RMSNorm: the fused gate/up + SwiGLU (2 x 14336 x 4096) and the
+    down projection (4096 x 14336), each over the rotating weight sets; and
+    config 1's 4096 x 4096 matvec over enough weight copies (~300 MB) that no
+    call is served by the Infinity Cache.  Bytes: codes, fp16 scales and zero
+    points, x read, y written."""
+    import torch
+
+    import mk.quant_ops as qo
+
+    G_h, G_i = HIDDEN // GROUP, INTER // GROUP
+    x = torch.randn((1, HIDDEN), device=dev).to(torch.float16)
+    m = torch.randn((1, INTER), device=dev).to(torch.float16)
+    fns = [lambda ws=ws: qo.q_gate_up_swiglu(x, ws[0][0], ws[1][0], ws[0][1], ws[1][1], ws[0][2], ws[1][2], bits=4,
+                                             group_size=GROUP) for ws in sets]
+    fns_d = [lambda ws=ws: qo.q4_matvec_decode(m, ws[2][0], ws[2][1], ws[2][2], group_size=GROUP) for ws in sets]
+    res = {}
+    for name, f, nb in (("gate_up_swiglu", fns, 2 * (INTER * HIDDEN // 2 + INTER * G_h * 4) + HIDDEN * 2 + INTER * 2),
+                        ("down", fns_d, HIDDEN * INTER // 2 + HIDDEN * G_i * 4 + INTER * 2 + HIDDEN * 2)):
+        ms = time_steps(f, steps, warmup)
+        res[name] = {"us_per_call": ms * 1e3, "hbm_gbs": nb / (ms * 1e-3) / 1e9,
+                     "frac_of_peak": nb / (ms * 1e-3) / 1e9 / PEAK_GBS, "bytes": nb}
+    gen = torch.Generator(device=dev).manual_seed(1)
+    c1 = []
+    for _ in range(32):
+        W = torch.randn((HIDDEN, HIDDEN), generator=gen, device=dev, dtype=torch.float32) * 0.02
+        c1.append(quantize_on_gpu(W, 4, GROUP))
+        del W
+    fns_1 = [lambda w=w: qo.q4_matvec_decode(x, w[0], w[1], w[2], group_size=GROUP) for w in c1]
+    b1 = HIDDEN * HIDDEN // 2 + HIDDEN * G_h * 4 + 2 * HIDDEN * 2
+    ms = time_steps(fns_1, max(steps, 2 * len(fns_1)), warmup)
+    res["config1_4096x4096"] = {"us_per_call": ms * 1e3, "hbm_gbs": b1 / (ms * 1e-3) / 1e9,
+                                "frac_of_peak": b1 / (ms * 1e-3) / 1e9 / PEAK_GBS, "bytes": b1}
+    del c1, fns, fns_d, fns_1
+    torch.cuda.empty_cache()
+    return res
+
+
 def run_workload(name, dev, args):
     """One workload alone (single-workload profiling runs)."""
     if name == "config3":
@@ -753,6 +795,8 @@ def run_workload(name, dev, args):
     if name == "stack":
         return decode_stack_config5(dev)
     sets = [make_mlp_set(dev, 4, 100 + i) for i in range(args.sets)]
+    if name == "gemv":
+        return {"workload": "q4_gemv_M1", **gemv_extra(dev, sets, max(60, args.steps // 3))}
     if name == "mlp_q8":
         return {"workload": "q8_mlp_M1", **mlp_extra(dev, sets, 1, 8, max(60, args.steps // 3))}
     M = int(name.split("_m")[1])
@@ -821,6 +865,7 @@ def main():
     if not args.no_extra:
         for bits, M in ((4, 4), (4, 8), (4, 32), (8, 1)):
             extra[f"q{bits}_mlp_M{M}"] = mlp_extra(dev, sets, M, bits, max(60, args.steps // 3))
+        extra["q4_gemv_M1"] = gemv_extra(dev, sets, max(60, args.steps // 3))
         torch.cuda.empty_cache()
         extra["paged_attention"] = attention_config3(dev, max(50, args.steps // 3), 10)
         extra["paged_attention_short"] = attention_short(dev)

@@ -1097,11 +1097,17 @@ __global__ __launch_bounds__(1024) void gemv_xk_kernel(const GemvArgs args) {
 // rows per workgroup (per matrix): 4 for gate/up (twice the workgroups of 8
 // rows keep more waves queued behind the resident ones, which shortens the
 // drain at the end of the launch), 8 for a single matrix (whose K-split over
-// up to 8 waves already gives each workgroup enough waves)
+// up to 8 waves already gives each workgroup enough waves).  A small q4
+// single-matrix launch at M = 1 -- under 2048 waves at 8 rows, i.e. fewer
+// than two per SIMD, such as 4096 x 4096 -- takes 4 rows instead (launch_dot;
+// measured 4096 x 4096 4.74 -> 4.35 us per call; the 4096 x 14336 down at 4
+// rows, 7168 waves, measured 9.8 against 8.8 us).
 template <int BITS, int NMAT>
 constexpr int dot_rows() {
   return NMAT == 2 ? 4 : 8;
 }
+constexpr int kDotSmallRows = 4;
+constexpr int kDotSmallWaves = 2048;
 constexpr int DOT_SZ_VEC = 2;  // 16-byte (s|z) vectors staged per lane
 constexpr int SEG_STRIDE = 64; // fp16 entries per staged (s|z) run
 
@@ -1196,11 +1202,10 @@ __device__ __forceinline__ float wave_total(float v) {
 // MR activation rows (1, 2 or 4; rows past M repeat row M - 1 and are not
 // stored) share each lane's code unpack: a batched decode step costs 4 MR
 // v_dot2 per 8 codes on top of the 5-instruction unpack.
-template <int BITS, int NMAT, int EPI, bool NORM, int MR>
+template <int BITS, int NMAT, int EPI, bool NORM, int MR, int R = dot_rows<BITS, NMAT>()>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void gemv_dot_kernel(
     const GemvArgs args) {
   static_assert(!NORM || MR == 1, "the norm prologue takes one activation row");
-  constexpr int R = dot_rows<BITS, NMAT>();
   constexpr int V = NMAT * R;  // values per activation row reduced per lane
   constexpr int VT = V * MR;   // values reduced per lane
   constexpr int NSEG = V * 2;  // (matrix, row, s|z) runs staged per wave
@@ -1754,9 +1759,8 @@ bool tile_eligible(const GemvArgs& a, int act_dt, int sc_dt) {
 template <bool NORM>
 inline int dot_row_groups(int kw) { return NORM ? (kw >= 2 ? 2 : 4) : 1; }
 
-template <int BITS, int NMAT, int EPI, bool NORM = false>
-int launch_dot(GemvArgs a, hipStream_t st) {
-  constexpr int R = dot_rows<BITS, NMAT>();
+template <int BITS, int NMAT, int EPI, bool NORM, int R>
+int launch_dot_rows(GemvArgs a, hipStream_t st) {
   a.rg = dot_row_groups<NORM>(a.kw);
   const int rows = R * a.rg;
   const dim3 grid((unsigned)((a.N + rows - 1) / rows));
@@ -1765,15 +1769,28 @@ int launch_dot(GemvArgs a, hipStream_t st) {
   const size_t lds = (NORM ? (size_t)a.K * 2 : 0) + stage_bytes;
   if constexpr (NORM) {
     MK_REQUIRE(a.K / 8 <= 2 * (int)block.x);  // the prologue's two 16-byte chunks per thread cover the row
-    gemv_dot_kernel<BITS, NMAT, EPI, true, 1><<<grid, block, lds, st>>>(a);
+    gemv_dot_kernel<BITS, NMAT, EPI, true, 1, R><<<grid, block, lds, st>>>(a);
   } else {
-    if (a.M <= 1) gemv_dot_kernel<BITS, NMAT, EPI, false, 1><<<grid, block, lds, st>>>(a);
-    else if (a.M == 2) gemv_dot_kernel<BITS, NMAT, EPI, false, 2><<<grid, block, lds, st>>>(a);
-    else if constexpr (BITS == 4) gemv_dot_kernel<BITS, NMAT, EPI, false, 4><<<grid, block, lds, st>>>(a);
+    if (a.M <= 1) gemv_dot_kernel<BITS, NMAT, EPI, false, 1, R><<<grid, block, lds, st>>>(a);
+    else if constexpr (R != dot_rows<BITS, NMAT>()) return MK_ERR_UNSUPPORTED;  // small-launch rows: M = 1 only
+    else if (a.M == 2) gemv_dot_kernel<BITS, NMAT, EPI, false, 2, R><<<grid, block, lds, st>>>(a);
+    else if constexpr (BITS == 4) gemv_dot_kernel<BITS, NMAT, EPI, false, 4, R><<<grid, block, lds, st>>>(a);
     else return MK_ERR_UNSUPPORTED;  // q8: at most two rows (four would spill)
   }
   MK_CHECK_LAUNCH();
   return MK_OK;
+}
+
+template <int BITS, int NMAT, int EPI, bool NORM = false>
+int launch_dot(GemvArgs a, hipStream_t st) {
+  constexpr int R = dot_rows<BITS, NMAT>();
+  if constexpr (BITS == 4 && NMAT == 1 && R > kDotSmallRows) {
+    // a q4 single matrix at M = 1 that would run under kDotSmallWaves waves
+    const int rg = dot_row_groups<NORM>(a.kw);
+    const int64_t waves = (int64_t)((a.N + R * rg - 1) / (R * rg)) * rg * a.kw;
+    if (a.M <= 1 && waves < kDotSmallWaves) return launch_dot_rows<BITS, NMAT, EPI, NORM, kDotSmallRows>(a, st);
+  }
+  return launch_dot_rows<BITS, NMAT, EPI, NORM, R>(a, st);
 }
 
 template <int BITS, typename AT, typename ST, int NMAT, int EPI>
