@@ -220,6 +220,25 @@ __device__ __forceinline__ bool argmax_better(float v, int64_t i, float bv, int6
   return v > bv || (v == bv && i < bi);
 }
 
+// (value, index) of the row's best entry from every thread -> out[row]
+__device__ __forceinline__ void argmax_finish(float bv, int64_t bi, int64_t n, int64_t* __restrict__ out) {
+  for (int d = 32; d >= 1; d >>= 1) {
+    const float ov = __shfl_xor(bv, d, 64);
+    const int64_t oi = __shfl_xor(bi, d, 64);
+    if (argmax_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  __shared__ float sv[16];
+  __shared__ int64_t si[16];
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { sv[wave] = bv; si[wave] = bi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+      if (argmax_better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
+    out[blockIdx.x] = bi < n ? bi : 0;
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(1024) void argmax_rows_kernel(const T* __restrict__ x, int64_t* __restrict__ out,
                                                            int64_t n, bool vec) {
@@ -259,21 +278,73 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const T* __restrict__
       if (argmax_better(v, i, bv, bi)) { bv = v; bi = i; }
     }
   }
-  for (int d = 32; d >= 1; d >>= 1) {
-    const float ov = __shfl_xor(bv, d, 64);
-    const int64_t oi = __shfl_xor(bi, d, 64);
-    if (argmax_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  argmax_finish(bv, bi, n, out);
+}
+
+// fp16 rows of whole 16-byte chunks (the logits of a decode step): a thread
+// takes a chunk's 8 values with packed fp16 ops -- the chunk maximum
+// (maxNum, so NaNs drop out of it), and a packed sum that is NaN whenever the
+// chunk holds a NaN (or both infinities, which the exact check below then
+// rules out) -- keeps the first chunk that raises its maximum, with its 16
+// bytes, and only at the end finds the first position of that maximum inside
+// it.  A chunk flagged by its sum is checked value by value for the first
+// NaN, which np.argmax's rule puts above every number.  16 loads per thread in
+// flight cover a 128256-entry row in one round.
+__global__ __launch_bounds__(1024) void argmax_rows_f16_kernel(const f16* __restrict__ x,
+                                                               int64_t* __restrict__ out, int64_t n) {
+  const f16* r = x + (size_t)blockIdx.x * n;
+  const int64_t nc = n / 8;
+  const int nt = blockDim.x;
+  f16 best = (f16)(-INFINITY);
+  int64_t bc = -1;         // this thread's chunk holding its first maximum
+  u32x4 bw = {0u, 0u, 0u, 0u};
+  int64_t nan_i = n;       // this thread's first NaN
+  constexpr int UNR = 16;
+  for (int64_t c0 = 0; c0 < nc; c0 += (int64_t)nt * UNR) {
+    u32x4 w[UNR];
+#pragma unroll
+    for (int j = 0; j < UNR; ++j) {
+      const int64_t c = c0 + (int64_t)j * nt + threadIdx.x;
+      w[j] = ldg128(r + 8 * (c < nc ? c : nc - 1));
+    }
+#pragma unroll
+    for (int j = 0; j < UNR; ++j) {
+      const int64_t c = c0 + (int64_t)j * nt + threadIdx.x;
+      if (c >= nc) continue;
+      const f16x2 a0 = bitcast<f16x2>(w[j][0]), a1 = bitcast<f16x2>(w[j][1]);
+      const f16x2 a2 = bitcast<f16x2>(w[j][2]), a3 = bitcast<f16x2>(w[j][3]);
+      const f16x2 m2 = __builtin_elementwise_max(__builtin_elementwise_max(a0, a1), __builtin_elementwise_max(a2, a3));
+      const f16 m = __builtin_elementwise_max(m2[0], m2[1]);
+      const f16x2 s2 = (a0 + a1) + (a2 + a3);
+      const f16 sum = s2[0] + s2[1];
+      if (sum != sum && nan_i == n) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t h = (w[j][e >> 1] >> (16 * (e & 1))) & 0x7FFFu;
+          if (h > 0x7C00u && nan_i == n) nan_i = 8 * c + e;
+        }
+      }
+      if (bc < 0 || m > best) {
+        best = m;
+        bc = c;
+        bw = w[j];
+      }
+    }
   }
-  __shared__ float sv[16];
-  __shared__ int64_t si[16];
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) { sv[wave] = bv; si[wave] = bi; }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < (nt >> 6); ++w)
-      if (argmax_better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
-    out[blockIdx.x] = bi < n ? bi : 0;
+  float bv = -INFINITY;
+  int64_t bi = n;
+  if (nan_i < n) {
+    bv = __builtin_nanf("");
+    bi = nan_i;
+  } else if (bc >= 0) {
+    int first = 7;
+#pragma unroll
+    for (int e = 7; e >= 0; --e)
+      if (bitcast<f16x2>(bw[e >> 1])[e & 1] == best) first = e;
+    bv = (float)best;
+    bi = 8 * bc + first;
   }
+  argmax_finish(bv, bi, n, out);
 }
 
 }  // namespace
@@ -288,7 +359,9 @@ int mk_argmax_rows(const void* x, int64_t* out, int64_t rows, int64_t n, int dty
   const size_t es = dtype == MK_DT_F32 ? 4 : 2;
   // every row starts 16-byte aligned and holds whole 16-byte chunks
   const bool vec = mk_aligned(x, 16) && ((size_t)n * es) % 16 == 0;
-  if (dtype == MK_DT_F16)
+  if (dtype == MK_DT_F16 && vec)
+    argmax_rows_f16_kernel<<<(unsigned)rows, 1024, 0, st>>>((const f16*)x, out, n);
+  else if (dtype == MK_DT_F16)
     argmax_rows_kernel<f16><<<(unsigned)rows, 1024, 0, st>>>((const f16*)x, out, n, vec);
   else if (dtype == MK_DT_BF16)
     argmax_rows_kernel<bf16><<<(unsigned)rows, 1024, 0, st>>>((const bf16*)x, out, n, vec);

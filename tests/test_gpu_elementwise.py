@@ -84,11 +84,14 @@ def test_swiglu_and_residual_add(dev, n, dt):
 
 @pytest.mark.parametrize("rows,n,dt", [(1, 128256, torch.float16), (32, 128256, torch.float16),
                                        (3, 1000, torch.bfloat16), (2, 515, torch.float16),
-                                       (4, 4096, torch.float32), (2, 7, torch.float32)])
+                                       (4, 4096, torch.float32), (2, 7, torch.float32),
+                                       (5, 40000, torch.float16), (5, 8, torch.float16)])
 def test_argmax_rows(dev, rows, n, dt):
     """Greedy sampling (models/sampling.py:120-124) on device against
-    np.argmax: random rows, planted ties (the first index must win) and a NaN
-    row (the first NaN wins, as in numpy)."""
+    np.argmax: random rows, planted ties (the first index must win), a NaN
+    row (the first NaN wins, as in numpy), a row with both infinities (whose
+    packed fp16 sums are NaN without a NaN in the row) and a row of signed
+    zeros (equal: the first wins)."""
     from mk.llama_stack_ops import greedy_sample
 
     rng = np.random.default_rng(rows * 7 + n)
@@ -98,6 +101,11 @@ def test_argmax_rows(dev, rows, n, dt):
     if rows > 2:
         x[2, n // 2] = np.nan
         x[2, n - 2] = np.nan
+    if rows > 4:
+        x[3, n // 4] = -np.inf
+        x[3, n - 1] = x[3, n // 5 + 1] = np.inf
+        x[4] = 0.0
+        x[4, ::3] = -0.0
     xt = torch.from_numpy(x).to(dt)
     want = np.argmax(xt.float().numpy(), axis=-1)  # the rounded values' argmax
     got = greedy_sample(xt.to(dev)).cpu().numpy()
