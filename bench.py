@@ -41,7 +41,7 @@ sys.path.insert(0, os.path.join(ROOT, "mlx-metal-kernels_amd"))
 
 PEAK_GBS = 8000.0
 HIDDEN, INTER, GROUP = 4096, 14336, 64
-DOMINANT_KERNEL = "gemv_dot_kernel<4, 2, 2, true, 1>"  # residual + RMSNorm + q4 gate/up + SwiGLU, M = 1
+DOMINANT_KERNEL = "gemv_dot_kernel<4, 2, 2, true, 1, 4>"  # residual + RMSNorm + q4 gate/up + SwiGLU, M = 1
 COPY_KERNEL_HINT = "copy"                      # torch's device-to-device copy kernel
 TRAFFIC_SUMMARY = "gemv_dot_q4_rmsnorm_gate_up_M1_traffic.json"
 ATTN_TRAFFIC_SUMMARY = "paged_attn_config3_fp16_traffic.json"
@@ -905,7 +905,7 @@ def main():
                    "step_bytes": step_bytes, "frac_of_peak": round(value / PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": load_traffic(),
-                     "kernel": "gemv_dot_kernel<4,2,2,true,1> residual+RMSNorm+q4 gate/up+SwiGLU 2x14336x4096 M=1",
+                     "kernel": "gemv_dot_kernel<4,2,2,true,1,4> residual+RMSNorm+q4 gate/up+SwiGLU 2x14336x4096 M=1",
                      "bytes_per_launch": b_front, "us_per_launch": round(ms_front * 1e3, 3)},
         "cpu_baseline": cpu,
         "extra": extra,
