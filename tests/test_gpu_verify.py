@@ -41,11 +41,14 @@ def _np16(a, dt):
 @pytest.mark.parametrize("B,W,Hq,Hkv,D,P,mb", [
     (1, 2, 32, 8, 128, 16, 8), (3, 4, 32, 8, 128, 16, 40), (5, 8, 32, 8, 128, 16, 24),
     (2, 4, 32, 8, 64, 16, 16), (4, 3, 8, 8, 64, 16, 12), (2, 8, 8, 1, 128, 16, 10),
-    (3, 5, 32, 4, 128, 8, 20), (2, 4, 16, 2, 96, 16, 6)])
+    (3, 5, 32, 4, 128, 8, 20), (2, 4, 16, 2, 96, 16, 6),
+    (1, 16, 8, 2, 64, 16, 12), (2, 33, 4, 1, 64, 16, 8), (1, 64, 4, 4, 128, 16, 10)])
 def test_verify_attention_vs_oracle(dev, dtype, B, W, Hq, Hkv, D, P, mb):
-    """GQA 32/8, MHA, MQA, a non-16 page size (LDS page list) and D = 96
-    (generic kernel); lengths include rows that see nothing (length < W) and
-    contexts split over several pairs."""
+    """GQA 32/8, MHA, MQA, a non-16 page size (LDS page list), D = 96
+    (generic kernel) and widths up to the limit of 64 (W·G rows of a kv head
+    over several 16-column blocks, the division-free row mapping at its
+    widest); lengths include rows that see nothing (length < W) and contexts
+    split over several pairs."""
     print(f"verify attention {dtype} B={B} W={W} Hq={Hq} Hkv={Hkv} D={D} P={P} mb={mb}", flush=True)
     rng = np.random.default_rng(7 * B + W + D)
     K, V, bt = _pages(rng, B, mb, P, Hkv, D)

@@ -101,3 +101,18 @@ def test_hip_verify_path_needs_a_device():
     bt = torch.zeros(1, 4, dtype=torch.int32)
     with pytest.raises((RuntimeError, ValueError)):
         sv.paged_verify_attention(q, K, K, bt, 64)
+
+
+def test_row_mapping_constant_divides_exactly():
+    """The verify kernels map a wave's virtual head h0 + j (j < 16) to its row
+    without a per-lane division: with x = h0 % W + j < W + 16, x // W is
+    (x * ceil(2^16 / W)) >> 16 for every width the entry points accept
+    (1..64); the entry points reject W = 65 and up.  Checked here against
+    integer division over the whole range; the identity has margin above the
+    accepted widths and first fails at W = 257."""
+    def ok(W):
+        magic = (65536 + W - 1) // W
+        return all((x * magic) >> 16 == x // W for x in range(W + 16))
+
+    assert all(ok(W) for W in range(1, 65))
+    assert next(W for W in range(65, 1025) if not ok(W)) == 257
